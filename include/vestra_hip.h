@@ -1,0 +1,267 @@
+/*
+ * vestra_hip.h -- C ABI of the MI355X (gfx950) HIP backend for the DA3-BASE
+ * ViT encoder hot path of hoppworks/vestra-kernels.
+ *
+ * The surface mirrors the crate's device API (`src/cuda.rs`): a runtime that
+ * owns one device and one ordered stream (CudaRuntime), opaque device-resident
+ * f32 tensors (CudaTensorF32), prepared projection weights (CudaLinearF32) and
+ * a status code per CudaError variant.  Every entry point cites the reference
+ * item it replaces.  Signatures use plain pointers and sizes only.
+ *
+ * Conventions
+ *  - Every call validates its arguments before any HIP call; on failure it
+ *    returns a non-zero vh_status, leaves outputs untouched and records a
+ *    thread-local message readable with vh_last_error().
+ *  - All device work is ordered on the runtime's stream and asynchronous;
+ *    vh_download_f32 / vh_q8_0_download / vh_runtime_synchronize synchronise.
+ *  - A runtime may be shared between host threads only with external
+ *    synchronisation (the reference's `&self` methods have the same rule).
+ *  - Tensors created by an entry point (out-parameters) are owned by the
+ *    caller and released with vh_tensor_free.
+ *  - Sizes are size_t end to end: there is no 2^32-element limit.
+ */
+#ifndef VESTRA_HIP_H
+#define VESTRA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* CudaError (src/cuda.rs:337-354), one code per variant. */
+typedef enum vh_status {
+    VH_OK = 0,
+    VH_ERR_INITIALIZE = 1,      /* CudaError::Initialize { device, detail } */
+    VH_ERR_UPLOAD = 2,          /* CudaError::Upload(String) */
+    VH_ERR_DOWNLOAD = 3,        /* CudaError::Download(String) */
+    VH_ERR_LENGTH_MISMATCH = 4, /* CudaError::LengthMismatch { destination, source_len } */
+    VH_ERR_KERNEL = 5,          /* CudaError::Kernel(String): bad shape or launch failure */
+    VH_ERR_BLAS = 6,            /* CudaError::Blas(String): GEMM / linear shape errors */
+    VH_ERR_INVALID_ARGUMENT = 7 /* null handle or pointer (unrepresentable in the Rust API) */
+} vh_status;
+
+typedef struct vh_runtime vh_runtime;     /* CudaRuntime (src/cuda.rs:357-379) */
+typedef struct vh_tensor vh_tensor;       /* CudaTensorF32 (src/cuda.rs:1283-1286) */
+typedef struct vh_linear vh_linear;       /* CudaLinearF32 (src/cuda.rs:1291-1298) */
+typedef struct vh_q8_tensor vh_q8_tensor; /* device rows of BlockQ8_0 (src/lib.rs:33-38) */
+typedef struct vh_block vh_block;         /* prepared DA3-BASE encoder block */
+
+/* ---- errors --------------------------------------------------------------- */
+/* Message of the calling thread's last failure ("" if none). */
+const char *vh_last_error(void);
+/* The two lengths carried by the last VH_ERR_LENGTH_MISMATCH
+ * (CudaError::LengthMismatch { destination, source_len }). */
+void vh_last_length_mismatch(size_t *destination, size_t *source_len);
+
+/* ---- runtime: CudaRuntime::new / device / stream / Clone / Drop ----------- */
+/* src/cuda.rs:383-465: binds `device`, creates its ordered stream. */
+vh_status vh_runtime_new(size_t device, vh_runtime **out);
+/* src/cuda.rs:357 #[derive(Clone)]: shares the same device and stream. */
+vh_status vh_runtime_clone(const vh_runtime *rt, vh_runtime **out);
+void vh_runtime_free(vh_runtime *rt);
+/* src/cuda.rs:467-470 */
+size_t vh_runtime_device(const vh_runtime *rt);
+/* src/cuda.rs:1276-1279 stream(): the hipStream_t every operation uses. */
+void *vh_runtime_stream(const vh_runtime *rt);
+/* Blocks until all work queued on the runtime's stream has finished. */
+vh_status vh_runtime_synchronize(const vh_runtime *rt);
+
+/* ---- tensors -------------------------------------------------------------- */
+/* src/cuda.rs:474-483 upload_f32 */
+vh_status vh_upload_f32(const vh_runtime *rt, const float *values, size_t len, vh_tensor **out);
+/* src/cuda.rs:487-491 download_f32: synchronising; out_len must equal len. */
+vh_status vh_download_f32(const vh_runtime *rt, const vh_tensor *tensor, float *out,
+                          size_t out_len);
+/* Uninitialised device tensor of `len` floats (caller-provided output buffers). */
+vh_status vh_tensor_alloc(const vh_runtime *rt, size_t len, vh_tensor **out);
+void vh_tensor_free(vh_tensor *tensor);
+/* src/cuda.rs:1349-1356 len / is_empty */
+size_t vh_tensor_len(const vh_tensor *tensor);
+int vh_tensor_is_empty(const vh_tensor *tensor);
+/* Raw device address, for interop with other device libraries. */
+float *vh_tensor_device_ptr(const vh_tensor *tensor);
+
+/* ---- copies / residual (src/cuda.rs:496-654) ------------------------------ */
+vh_status vh_copy_f32(const vh_runtime *rt, const vh_tensor *source, vh_tensor **out);
+vh_status vh_copy_segment_f32(const vh_runtime *rt, const vh_tensor *source, size_t source_offset,
+                              size_t len, vh_tensor **out);
+vh_status vh_copy_segment_into_f32(const vh_runtime *rt, vh_tensor *destination,
+                                   size_t destination_offset, const vh_tensor *source,
+                                   size_t source_offset, size_t len);
+vh_status vh_overwrite_prefix_f32(const vh_runtime *rt, vh_tensor *destination,
+                                  const vh_tensor *source, size_t len);
+/* src/cuda.rs:630-654 add_f32_in_place: destination += source. */
+vh_status vh_add_f32_in_place(const vh_runtime *rt, vh_tensor *destination,
+                              const vh_tensor *source);
+
+/* ---- GEMM and epilogues --------------------------------------------------- */
+/* src/cuda.rs:661-704 gemm_row_major_f32: C[m,n] = A[m,k] x B[k,n], row-major.
+ * fp32 MFMA kernel (replaces cublasSgemm). */
+vh_status vh_gemm_row_major_f32(const vh_runtime *rt, const vh_tensor *a, const vh_tensor *b,
+                                size_t m, size_t k, size_t n, vh_tensor **out);
+/* src/cuda.rs:708-742 bias_scale_f32_in_place: v = (v + bias[c]) * gamma[c]. */
+vh_status vh_bias_scale_f32_in_place(const vh_runtime *rt, vh_tensor *values,
+                                     const vh_tensor *bias, const vh_tensor *gamma, size_t rows,
+                                     size_t columns);
+/* src/cuda.rs:747-759 gelu_f32_in_place (arithmetic of Kernels::gelu,
+ * src/dispatch.rs:56-73: AVX-512 erf/exp form, scalar form on the n%16 tail). */
+vh_status vh_gelu_f32_in_place(const vh_runtime *rt, vh_tensor *values);
+
+/* ---- LayerNorm ------------------------------------------------------------ */
+/* src/cuda.rs:764-810 layernorm_f32 (one wave64 per row). */
+vh_status vh_layernorm_f32(const vh_runtime *rt, const vh_tensor *input, const vh_tensor *gamma,
+                           const vh_tensor *beta, size_t rows, size_t columns, float epsilon,
+                           vh_tensor **out);
+/* src/cuda.rs:815-863 layernorm_f32_cpu_order: the scalar::layernorm order,
+ * bit-exact with src/scalar.rs:99-114. */
+vh_status vh_layernorm_f32_cpu_order(const vh_runtime *rt, const vh_tensor *input,
+                                     const vh_tensor *gamma, const vh_tensor *beta, size_t rows,
+                                     size_t columns, float epsilon, vh_tensor **out);
+
+/* ---- attention ------------------------------------------------------------ */
+/* src/cuda.rs:868-922 attention_online_f32: head-major [heads,tokens,head_dim]
+ * in and out, 1 <= head_dim <= 64, scale 1/sqrt(head_dim). */
+vh_status vh_attention_online_f32(const vh_runtime *rt, const vh_tensor *q, const vh_tensor *k,
+                                  const vh_tensor *v, size_t heads, size_t tokens,
+                                  size_t head_dim, vh_tensor **out);
+/* flash_attention_f32_da3_base (src/lib.rs:82-91, src/specialized.rs:730-765):
+ * head_dim 64, scale 1/8, fp32-MFMA online softmax.  Any token count is
+ * accepted (the reference's tokens % 865 gate is a CPU-kernel limit).
+ * token_major = 0 writes head-major [heads,tokens,64]; 1 writes token-major
+ * [tokens, heads*64] (the fused hnd_to_token of src/cuda.rs:984-1036). */
+vh_status vh_flash_attention_f32_da3_base(const vh_runtime *rt, const vh_tensor *q,
+                                          const vh_tensor *k, const vh_tensor *v, size_t heads,
+                                          size_t tokens, int token_major, vh_tensor **out);
+
+/* ---- layout (src/cuda.rs:927-1175) ---------------------------------------- */
+vh_status vh_split_qkv_hnd_f32(const vh_runtime *rt, const vh_tensor *qkv, size_t tokens,
+                               size_t heads, size_t head_dim, vh_tensor **q, vh_tensor **k,
+                               vh_tensor **v);
+vh_status vh_hnd_to_token_f32(const vh_runtime *rt, const vh_tensor *hnd, size_t tokens,
+                              size_t heads, size_t head_dim, vh_tensor **out);
+vh_status vh_token_to_chw_f32(const vh_runtime *rt, const vh_tensor *token_major, size_t tokens,
+                              size_t channels, vh_tensor **out);
+vh_status vh_patchify_nchw_f32(const vh_runtime *rt, const vh_tensor *image, size_t height,
+                               size_t width, size_t patch, size_t channels, vh_tensor **out);
+vh_status vh_prepend_cls_add_pos_f32(const vh_runtime *rt, const vh_tensor *patches,
+                                     const vh_tensor *cls, const vh_tensor *position,
+                                     size_t patch_count, size_t embed, vh_tensor **out);
+
+/* ---- RoPE ----------------------------------------------------------------- */
+/* rope::rope2d (src/rope.rs:30-80) on a device [heads, n, head_dim] tensor.
+ * pos_yx is host int64 [n*2]; the sin/cos table is built on the host with
+ * the same libm calls as the reference and cached on the runtime. */
+vh_status vh_rope2d_f32_in_place(const vh_runtime *rt, vh_tensor *x, size_t heads, size_t n,
+                                 size_t head_dim, const int64_t *pos_yx, float frequency);
+/* src/cuda.rs:1178-1228 qk_norm_rope_f32_da3_base: 64-wide rows, device
+ * positions_yx f32 [tokens*2], rotation table as src/specialized.rs:389-410. */
+vh_status vh_qk_norm_rope_f32_da3_base(const vh_runtime *rt, vh_tensor *q, vh_tensor *k,
+                                       const vh_tensor *q_gamma, const vh_tensor *q_beta,
+                                       const vh_tensor *k_gamma, const vh_tensor *k_beta,
+                                       const vh_tensor *positions_yx, size_t heads,
+                                       size_t tokens, float frequency, float epsilon);
+
+/* ---- prepared projections (CudaLinearF32) --------------------------------- */
+/* src/cuda.rs:1230-1268 prepare_linear_f32: weight row-major [K, N], bias [N],
+ * gamma [N] or NULL (unit).  Weights are repacked once for the MFMA kernel. */
+vh_status vh_prepare_linear_f32(const vh_runtime *rt, size_t input_features,
+                                size_t output_features, const float *weight, const float *bias,
+                                const float *gamma, vh_linear **out);
+void vh_linear_free(vh_linear *linear);
+size_t vh_linear_input_features(const vh_linear *linear);  /* src/cuda.rs:1301-1304 */
+size_t vh_linear_output_features(const vh_linear *linear); /* src/cuda.rs:1306-1309 */
+/* src/cuda.rs:1312-1334 run: (input x W + bias) * gamma, one fused launch. */
+vh_status vh_linear_run(const vh_linear *linear, const vh_tensor *input, size_t rows,
+                        vh_tensor **out);
+/* src/cuda.rs:1340-1344 run_chw: run, then token-major -> CHW. */
+vh_status vh_linear_run_chw(const vh_linear *linear, const vh_tensor *input, size_t rows,
+                            vh_tensor **out);
+/* run + gelu_f32_in_place fused (the fc1 step; src/gemm.rs:70-96 order:
+ * GEMM, + bias, then GELU).  gamma must be unit (prepared with NULL). */
+vh_status vh_linear_run_gelu(const vh_linear *linear, const vh_tensor *input, size_t rows,
+                             vh_tensor **out);
+/* run + add_f32_in_place fused (out-projection / fc2 with LayerScale and the
+ * residual, src/specialized.rs:811-929 then src/dispatch.rs:77-83):
+ * residual += (input x W + bias) * gamma. */
+vh_status vh_linear_run_residual(const vh_linear *linear, const vh_tensor *input, size_t rows,
+                                 vh_tensor *residual);
+/* qkv_f32_da3_base (src/specialized.rs:996-1167) as a device op on a linear
+ * with N = 3*heads*64: Q/K/V written head-major [images][heads][tokens][64]
+ * with bias; when pos_yx (host int64 [tokens*2]) is non-NULL the 2-D RoPE of
+ * src/rope.rs:30-93 is applied to Q and K in the same launch.  rows must be
+ * images * tokens. */
+vh_status vh_linear_run_qkv_hnd(const vh_linear *linear, const vh_tensor *input, size_t images,
+                                size_t tokens, size_t heads, const int64_t *pos_yx,
+                                float frequency, vh_tensor **q, vh_tensor **k, vh_tensor **v);
+
+/* ---- Q8_0 ------------------------------------------------------------------ */
+/* Rows of BlockQ8_0 ({f16 d; i8 qs[32]}, 34 bytes, src/lib.rs:33-38) held on
+ * the device as separate qs and d arrays. */
+vh_status vh_q8_0_upload(const vh_runtime *rt, const void *blocks, size_t rows, size_t k,
+                         vh_q8_tensor **out);
+/* Writes rows*k/32 BlockQ8_0 values (AoS) to `blocks`; synchronising. */
+vh_status vh_q8_0_download(const vh_runtime *rt, const vh_q8_tensor *tensor, void *blocks,
+                           size_t nblocks);
+void vh_q8_tensor_free(vh_q8_tensor *tensor);
+size_t vh_q8_tensor_rows(const vh_q8_tensor *tensor);
+size_t vh_q8_tensor_k(const vh_q8_tensor *tensor);
+/* quantize_row_q8_0 (src/q8_0_dot.rs:27-46) over each row of a device
+ * [rows, k] f32 tensor, k % 32 == 0.  Bit-exact. */
+vh_status vh_quantize_q8_0(const vh_runtime *rt, const vh_tensor *x, size_t rows, size_t k,
+                           vh_q8_tensor **out);
+/* Kernels::gemm_q8_0 (src/dispatch.rs:91-105, oracle src/scalar.rs:25-56):
+ * C[m,n] = sum_b (d_a*d_b)*isum_b with a_q [m,k] and b_q [n,k]; int8 MFMA
+ * block sums, f32 combine in block order.  Bit-exact. */
+vh_status vh_gemm_q8_0(const vh_runtime *rt, const vh_q8_tensor *a_q, const vh_q8_tensor *b_q,
+                       size_t m, size_t n, size_t k, vh_tensor **out);
+
+/* ---- DA3-BASE encoder block ------------------------------------------------ */
+/* Host pointers to one block's parameters, row-major [in, out] weights. */
+typedef struct vh_block_params {
+    const float *ln1_gamma, *ln1_beta; /* [768] */
+    const float *w_qkv, *b_qkv;        /* [768*2304], [2304] */
+    const float *w_proj, *b_proj;      /* [768*768], [768] */
+    const float *ls1;                  /* [768] LayerScale */
+    const float *ln2_gamma, *ln2_beta; /* [768] */
+    const float *w_fc1, *b_fc1;        /* [768*3072], [3072] */
+    const float *w_fc2, *b_fc2;        /* [3072*768], [768] */
+    const float *ls2;                  /* [768] */
+} vh_block_params;
+
+/* Uploads and repacks one block's weights (model-load time). */
+vh_status vh_block_prepare(const vh_runtime *rt, const vh_block_params *params, vh_block **out);
+void vh_block_free(vh_block *block);
+/* One pre-LN DA3-BASE block in place on x [images*tokens*768]: LN, QKV (+bias,
+ * + 2-D RoPE when pos_yx != NULL), attention, out-proj (+bias, *ls1) +
+ * residual, LN, fc1 (+bias, GELU), fc2 (+bias, *ls2) + residual.  The CPU
+ * composition it replaces chains src/scalar.rs:83, src/specialized.rs:996,
+ * src/rope.rs:30, src/attention.rs:66, src/specialized.rs:811,
+ * src/dispatch.rs:77, src/specialized.rs:770, src/scalar.rs:65 and
+ * src/dispatch.rs:56. */
+vh_status vh_vit_block_run(const vh_runtime *rt, const vh_block *block, vh_tensor *x,
+                           size_t images, size_t tokens, const int64_t *pos_yx,
+                           float rope_frequency, float epsilon);
+/* `layers` blocks in sequence (the 12-layer encoder). */
+vh_status vh_encoder_run(const vh_runtime *rt, const vh_block *const *blocks, size_t layers,
+                         vh_tensor *x, size_t images, size_t tokens, const int64_t *pos_yx,
+                         float rope_frequency, float epsilon);
+
+/* ---- profiling (device twin of DA3_FLASH_PROFILE, src/specialized.rs:1324) - */
+/* When enabled, every kernel launch is bracketed by HIP events on the
+ * runtime's stream and its duration accumulated under the kernel's name. */
+vh_status vh_profile_enable(vh_runtime *rt, int enabled);
+vh_status vh_profile_reset(vh_runtime *rt);
+/* Synchronises, then writes "name count total_ms\n" lines (NUL-terminated,
+ * truncated to buflen). */
+vh_status vh_profile_report(vh_runtime *rt, char *buf, size_t buflen);
+/* Stream-ordered wall clock: start records an event, stop records another,
+ * synchronises and returns the elapsed milliseconds. */
+vh_status vh_timer_start(vh_runtime *rt);
+vh_status vh_timer_stop(vh_runtime *rt, float *elapsed_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,367 @@
+"""GPU parity of the C-ABI device operators against the reference's device
+KATs (src/cuda.rs:1370-1607) and the CPU oracle.
+
+Bars: bit-exact for layout, copies, residual adds, RoPE with host tables,
+CPU-order LayerNorm and Q8_0; the reference's own tolerances elsewhere.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import vestra_hip as vh
+from conftest import assert_bits_equal, max_rel
+from vestra_hip import da3, seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def deterministic_values(n, seed):
+    """src/cuda.rs:1363-1367: sin(i*0.017578125 + seed)*0.75 + 0.1 in f32."""
+    i = np.arange(n, dtype=np.float32)
+    return ((np.sin((i * np.float32(0.017578125) + np.float32(seed)).astype(np.float32))
+             .astype(np.float32) * np.float32(0.75)) + np.float32(0.1)).astype(np.float32)
+
+
+# ---- src/cuda.rs:1370-1607 driver round trip and KATs ----------------------
+
+def test_round_trip_add_copy_segments(rt):
+    t = rt.upload_f32([1.0, -2.0, 3.5])
+    add = rt.upload_f32([0.5, 2.0, -1.0])
+    assert len(t) == 3 and not t.is_empty()
+    rt.add_f32_in_place(t, add)
+    assert rt.download_f32(t).tolist() == [1.5, 0.0, 2.5]
+    src = rt.upload_f32([9.0, 8.0, 7.0, 6.0])
+    copied = rt.copy_f32(src)
+    rt.overwrite_prefix_f32(copied, rt.upload_f32([-1.0, -2.0]), 2)
+    assert rt.download_f32(copied).tolist() == [-1.0, -2.0, 7.0, 6.0]
+    seg = rt.copy_segment_f32(src, 1, 2)
+    assert rt.download_f32(seg).tolist() == [8.0, 7.0]
+    rt.copy_segment_into_f32(copied, 2, seg, 0, 2)
+    assert rt.download_f32(copied).tolist() == [-1.0, -2.0, 8.0, 7.0]
+
+
+def test_gemm_bias_scale_linear_chain_kats(rt):
+    left = rt.upload_f32([1, 2, 3, 4, 5, 6])
+    right = rt.upload_f32([7, 8, 9, 10, 11, 12])
+    prod = rt.gemm_row_major_f32(left, right, 2, 3, 2)
+    assert rt.download_f32(prod).tolist() == [58.0, 64.0, 139.0, 154.0]
+    rt.bias_scale_f32_in_place(prod, rt.upload_f32([1.0, -4.0]), rt.upload_f32([0.5, 2.0]), 2, 2)
+    assert rt.download_f32(prod).tolist() == [29.5, 120.0, 70.0, 300.0]
+    first = rt.prepare_linear_f32(3, 2, [7, 8, 9, 10, 11, 12], [1.0, -4.0], [0.5, 2.0])
+    second = rt.prepare_linear_f32(2, 1, [2.0, -1.0], [3.0])
+    chained = second.run(first.run(left, 2), 2)
+    assert rt.download_f32(chained).tolist() == [-58.0, -157.0]
+    assert rt.download_f32(first.run_chw(left, 2)).tolist() == [29.5, 70.0, 120.0, 300.0]
+    assert first.input_features() == 3 and first.output_features() == 2
+
+
+def test_gelu_kat_within_2e6_of_scalar(rt):
+    x = np.array([-3.0, -1.0, 0.0, 1.0, 3.0], np.float32)
+    t = rt.upload_f32(x)
+    rt.gelu_f32_in_place(t)
+    assert np.abs(rt.download_f32(t) - O.gelu(x)).max() <= 2e-6
+
+
+def test_layernorm_kats(rt):
+    x = [1.0, 2.0, 5.0, -2.0, 3.0, 4.0]
+    g, b = [1.5, 0.5, 2.0], [-1.0, 0.25, 2.0]
+    exp = O.layernorm(x, 2, 3, g, b, 1e-5)
+    xt, gt, bt = rt.upload_f32(x), rt.upload_f32(g), rt.upload_f32(b)
+    assert np.abs(rt.download_f32(rt.layernorm_f32(xt, gt, bt, 2, 3, 1e-5)) - exp).max() <= 2e-5
+    cpu = rt.download_f32(rt.layernorm_f32_cpu_order(xt, gt, bt, 2, 3, 1e-5))
+    assert np.abs(cpu - exp).max() <= 2e-6
+    assert_bits_equal(cpu, exp, "cpu-order LayerNorm")
+
+
+def test_small_online_attention_vs_naive(rt):
+    heads, tokens, hd = 2, 5, 4
+    idx = np.arange(heads * tokens * hd, dtype=np.float32)
+
+    def vals(seed):
+        return np.sin(idx * np.float32(0.03125) + np.float32(seed)).astype(np.float32)
+
+    q, k, v = vals(0.1), vals(-0.2), vals(0.7)
+    exp = O.attention_naive(q, k, v, heads, tokens, hd)
+    out = rt.attention_online_f32(rt.upload_f32(q), rt.upload_f32(k), rt.upload_f32(v), heads,
+                                  tokens, hd)
+    assert np.abs(rt.download_f32(out) - exp).max() <= 5e-5
+
+
+def test_layout_split_unpack_chw(rt):
+    T, H, Dh = 3, 2, 4
+    E = H * Dh
+    qkv = deterministic_values(T * 3 * E, -0.4)
+    q, k, v = rt.split_qkv_hnd_f32(rt.upload_f32(qkv), T, H, Dh)
+    eq, ek, ev = O.split_qkv_hnd(qkv, T, H, Dh)
+    assert_bits_equal(rt.download_f32(q), eq, "split q")
+    assert_bits_equal(rt.download_f32(k), ek, "split k")
+    assert_bits_equal(rt.download_f32(v), ev, "split v")
+    tm = rt.hnd_to_token_f32(q, T, H, Dh)
+    etm = O.hnd_to_token(eq, T, H, Dh)
+    assert_bits_equal(rt.download_f32(tm), etm, "hnd_to_token")
+    chw = rt.download_f32(rt.token_to_chw_f32(tm, T, E))
+    assert_bits_equal(chw, etm.reshape(T, E).T.reshape(-1), "token_to_chw")
+
+
+def test_patchify_and_token_assembly_kats(rt):
+    image = rt.upload_f32(np.arange(48, dtype=np.float32))
+    patches = rt.download_f32(rt.patchify_nchw_f32(image, 4, 4, 2, 3))
+    assert patches.tolist() == [
+        0, 1, 4, 5, 16, 17, 20, 21, 32, 33, 36, 37, 2, 3, 6, 7, 18, 19, 22, 23, 34, 35, 38, 39,
+        8, 9, 12, 13, 24, 25, 28, 29, 40, 41, 44, 45, 10, 11, 14, 15, 26, 27, 30, 31, 42, 43, 46,
+        47]
+    toks = rt.prepend_cls_add_pos_f32(rt.upload_f32([10, 20, 30, 40]), rt.upload_f32([1, 2]),
+                                      rt.upload_f32([0.5, -0.5, 1.0, 2.0, -1.0, 3.0]), 2, 2)
+    assert rt.download_f32(toks).tolist() == [1.5, 1.5, 11.0, 22.0, 29.0, 43.0]
+
+
+# ---- error contract (CudaError variants, validation before launch) ---------
+
+def test_errors_before_launch(rt):
+    a = rt.upload_f32([1.0, 2.0, 3.0])
+    b = rt.upload_f32([1.0, 2.0])
+    with pytest.raises(vh.LengthMismatch) as e:
+        rt.add_f32_in_place(a, b)
+    assert (e.value.destination, e.value.source_len) == (3, 2)
+    with pytest.raises(vh.BlasError):
+        rt.gemm_row_major_f32(a, b, 2, 2, 2)
+    with pytest.raises(vh.KernelError):
+        rt.attention_online_f32(a, a, a, 1, 1, 65)
+    with pytest.raises(vh.KernelError):
+        rt.patchify_nchw_f32(a, 3, 1, 2, 1)
+    with pytest.raises(vh.LengthMismatch):
+        rt.copy_segment_f32(a, 2, 2)
+    lin = rt.prepare_linear_f32(2, 1, [1.0, 2.0], [0.0])
+    with pytest.raises(vh.BlasError):
+        lin.run(a, 2)
+    assert rt.download_f32(a).tolist() == [1.0, 2.0, 3.0]  # untouched
+
+
+# ---- GEMM (fp32 MFMA) -------------------------------------------------------
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 5, 3), (865, 768, 768), (33, 96, 130),
+                                   (64, 32, 64), (129, 67, 257)])
+def test_gemm_row_major_matches_float64(rt, m, k, n):
+    a = seeded.normal(101 + m, m * k)
+    b = seeded.normal(202 + n, k * n)
+    c = rt.download_f32(rt.gemm_row_major_f32(rt.upload_f32(a), rt.upload_f32(b), m, k, n))
+    ref = a.reshape(m, k).astype(np.float64) @ b.reshape(k, n).astype(np.float64)
+    # fp32 accumulation of K products: |err| <= K * eps * sum|a||b| bounds it.
+    bound = k * 6e-8 * (np.abs(a.reshape(m, k)).astype(np.float64) @ np.abs(b.reshape(k, n)))
+    assert np.all(np.abs(c.reshape(m, n) - ref) <= bound + 1e-30)
+
+
+@pytest.mark.parametrize("k,n", [(768, 2304), (768, 768), (768, 3072), (3072, 768)])
+def test_da3_projection_shapes_vs_oracle(rt, k, n):
+    m = 865
+    a = seeded.normal(11, m * k)
+    w = seeded.normal(12, k * n, 0.02)
+    bias = seeded.normal(13, n, 0.01)
+    scale = (0.75 + np.cos(np.arange(n) * 0.011)).astype(np.float32)
+    exp = O.linear_bias_scale(a, w, bias, scale, m, n, k)
+    lin = rt.prepare_linear_f32(k, n, w, bias, scale)
+    got = rt.download_f32(lin.run(rt.upload_f32(a), m))
+    assert max_rel(got, exp) <= 1e-5
+
+
+def test_fc1_gelu_epilogue_vs_oracle(rt):
+    m, k, n = 865, 768, 3072
+    a = seeded.normal(21, m * k)
+    w = seeded.normal(22, k * n, 0.02)
+    bias = seeded.normal(23, n, 0.02)
+    f = O.linear(a, w, m, n, k)
+    f = O.add_bias_rows(f, m, n, bias)
+    exp = O.gelu_avx512_lanes(f)
+    lin = rt.prepare_linear_f32(k, n, w, bias)
+    got = rt.download_f32(lin.run_gelu(rt.upload_f32(a), m))
+    assert max_rel(got, exp) <= 1e-5
+
+
+def test_residual_epilogue_vs_oracle(rt):
+    m, k, n = 865, 3072, 768
+    a = seeded.normal(31, m * k)
+    w = seeded.normal(32, k * n, 0.02)
+    bias = seeded.normal(33, n, 0.02)
+    ls = np.full(n, 0.5, np.float32)
+    x = seeded.normal(34, m * n)
+    y = O.linear_bias_scale(a, w, bias, ls, m, n, k)
+    exp = O.kernels_add(x, y)
+    lin = rt.prepare_linear_f32(k, n, w, bias, ls)
+    xt = rt.upload_f32(x)
+    lin.run_residual(rt.upload_f32(a), m, xt)
+    assert max_rel(rt.download_f32(xt) - x, y) <= 1e-5
+    assert max_rel(rt.download_f32(xt), exp) <= 1e-6
+
+
+@pytest.mark.parametrize("rope", [False, True])
+def test_qkv_head_major_rope_vs_oracle(rt, rope):
+    T = 865
+    a = seeded.normal(41, T * 768)
+    w = seeded.normal(42, 768 * 2304, 0.02)
+    bias = seeded.normal(43, 2304, 0.02)
+    pos = da3.positions_yx(24, 36)
+    eq, ek, ev = O.qkv(a, w, bias, T)
+    if rope:
+        eq = O.rope2d(eq, 12, T, 64, pos, 100.0)
+        ek = O.rope2d(ek, 12, T, 64, pos, 100.0)
+    lin = rt.prepare_linear_f32(768, 2304, w, bias)
+    q, k, v = lin.run_qkv_hnd(rt.upload_f32(a), 1, T, 12, pos if rope else None, 100.0)
+    for got, exp, name in ((q, eq, "q"), (k, ek, "k"), (v, ev, "v")):
+        assert max_rel(rt.download_f32(got), exp) <= 1e-5, name
+
+
+# ---- attention ---------------------------------------------------------------
+
+@pytest.mark.parametrize("heads,n,hd,seed", [(2, 8, 16, 0x12345678), (4, 37, 32, 0xDEADBEEF),
+                                             (1, 130, 8, 0x0BADF00D), (3, 71, 64, 0xA7710001)])
+def test_online_attention_matches_naive_cases(rt, heads, n, hd, seed):
+    """tests/attention_matches_naive.rs:21-58 cases, |diff| < 1e-4."""
+    vals = seeded.xorshift32_values(3 * heads * n * hd, seed)
+    q, k, v = np.split(vals, 3)
+    exp = O.attention_naive(q, k, v, heads, n, hd)
+    got = rt.download_f32(rt.attention_online_f32(rt.upload_f32(q), rt.upload_f32(k),
+                                                  rt.upload_f32(v), heads, n, hd))
+    assert np.abs(got - exp).max() < 1e-4
+
+
+def test_flash_da3_production_shape_vs_oracle(rt):
+    """src/cuda.rs:1612-1650: 12 x 865 x 64, MAE <= 5e-5 and max <= 5e-4 against
+    attention(); the parity bar here is the tighter max-relative 1e-4."""
+    H, T = 12, 865
+    n = H * T * 64
+    q, k, v = deterministic_values(n, 0.1), deterministic_values(n, -0.3), deterministic_values(n, 0.7)
+    exp = O.attention(q, k, v, H, T, 64)
+    got = rt.download_f32(rt.flash_attention_f32_da3_base(rt.upload_f32(q), rt.upload_f32(k),
+                                                          rt.upload_f32(v), H, T))
+    err = np.abs(got - exp)
+    assert err.mean() <= 5e-5 and err.max() <= 5e-4
+    assert max_rel(got, exp) <= 1e-4
+
+
+def test_flash_config1_normal_inputs_token_major(rt):
+    """Q, K, V ~ N(0,1), 12 heads x 865 x 64, out [865, 768]."""
+    H, T = 12, 865
+    n = H * T * 64
+    q, k, v = seeded.normal(1, n), seeded.normal(2, n), seeded.normal(3, n)
+    exp = O.hnd_to_token(O.attention(q, k, v, H, T, 64), T, H, 64)
+    got = rt.download_f32(rt.flash_attention_f32_da3_base(rt.upload_f32(q), rt.upload_f32(k),
+                                                          rt.upload_f32(v), H, T, True))
+    assert max_rel(got, exp) <= 1e-4
+
+
+def test_flash_two_view_window_vs_serial(rt):
+    """src/specialized.rs:2871-2910: 1 head x 2*865 tokens, MAE <= 2e-5, max <= 2e-4."""
+    T = 2 * 865
+    i = np.arange(T * 64, dtype=np.float32)
+    q = np.sin(i * np.float32(0.013)).astype(np.float32)
+    k = np.cos(i * np.float32(0.007)).astype(np.float32)
+    v = np.sin(i * np.float32(0.017)).astype(np.float32)
+    exp = O.attention_serial(q, k, v, 1, T, 64)
+    got = rt.download_f32(rt.flash_attention_f32_da3_base(rt.upload_f32(q), rt.upload_f32(k),
+                                                          rt.upload_f32(v), 1, T))
+    err = np.abs(got - exp)
+    assert err.mean() <= 2e-5 and err.max() <= 2e-4
+
+
+@pytest.mark.parametrize("T", [1, 63, 64, 65, 3457])
+def test_flash_ragged_token_counts(rt, T):
+    H = 2
+    n = H * T * 64
+    q, k, v = seeded.normal(5 + T, n), seeded.normal(6 + T, n), seeded.normal(7 + T, n)
+    exp = O.attention_naive(q, k, v, H, T, 64)
+    got = rt.download_f32(rt.flash_attention_f32_da3_base(rt.upload_f32(q), rt.upload_f32(k),
+                                                          rt.upload_f32(v), H, T))
+    assert max_rel(got, exp) <= 1e-4
+
+
+# ---- LayerNorm / GELU / RoPE ---------------------------------------------------
+
+def test_layernorm_da3_shape(rt):
+    rows, cols = 865, 768
+    x = seeded.normal(51, rows * cols)
+    g = seeded.normal(52, cols, 0.1, 1.0)
+    b = seeded.normal(53, cols, 0.1)
+    exp = O.layernorm(x, rows, cols, g, b, 1e-6)
+    xt, gt, bt = rt.upload_f32(x), rt.upload_f32(g), rt.upload_f32(b)
+    assert max_rel(rt.download_f32(rt.layernorm_f32(xt, gt, bt, rows, cols, 1e-6)), exp) <= 1e-5
+    cpu = rt.download_f32(rt.layernorm_f32_cpu_order(xt, gt, bt, rows, cols, 1e-6))
+    assert_bits_equal(cpu, exp, "cpu-order LayerNorm at 865x768")
+
+
+@pytest.mark.parametrize("n", [1000, 2657280, 17])
+def test_gelu_vs_kernels_gelu(rt, n):
+    """tests/simd_matches_scalar.rs ramp plus the fc1 size; AVX-512 form on
+    the n - n%16 prefix, scalar form on the tail."""
+    x = (np.arange(n, dtype=np.float32) * np.float32(0.017) - np.float32(3.0)) if n == 1000 \
+        else seeded.normal(60 + n, n, 2.0)
+    exp = O.gelu_avx512_lanes(x)
+    t = rt.upload_f32(x)
+    rt.gelu_f32_in_place(t)
+    got = rt.download_f32(t)
+    main = n - n % 16
+    assert_bits_equal(got[:main], exp[:main], "AVX-512-form GELU")
+    assert np.abs(got[main:] - exp[main:]).max(initial=0.0) <= 2e-6
+
+
+def test_rope2d_bit_exact_with_host_table(rt):
+    H, T = 12, 865
+    x = seeded.normal(71, H * T * 64)
+    pos = da3.positions_yx(24, 36)
+    exp = O.rope2d(x, H, T, 64, pos, 100.0)
+    t = rt.upload_f32(x)
+    rt.rope2d_f32_in_place(t, H, T, 64, pos, 100.0)
+    assert_bits_equal(rt.download_f32(t), exp, "rope2d")
+    # src/rope.rs:133-154 small case: positions (i, 3i), head_dim 16
+    x2 = ((np.arange(3 * 7 * 16, dtype=np.float32) - 43.0) * 0.0625).astype(np.float32)
+    pos2 = np.array([[i, 3 * i] for i in range(7)], np.int64).reshape(-1)
+    t2 = rt.upload_f32(x2)
+    rt.rope2d_f32_in_place(t2, 3, 7, 16, pos2, 100.0)
+    assert_bits_equal(rt.download_f32(t2), O.rope2d(x2, 3, 7, 16, pos2, 100.0), "rope2d small")
+
+
+def test_qk_norm_rope_production_shape(rt):
+    """src/cuda.rs:1652-1733: MAE <= 5e-5, max <= 5e-4 for Q and K."""
+    H, T, Dm = 12, 865, 64
+    n = H * T * Dm
+    src = deterministic_values(n, 0.21)
+    ksrc = deterministic_values(n, -0.37)
+    qg, qb = deterministic_values(Dm, 0.11), deterministic_values(Dm, -0.15)
+    kg, kb = deterministic_values(Dm, 0.31), deterministic_values(Dm, -0.23)
+    pos = da3.positions_yx(24, 36)
+    eq, ek = O.qk_norm_rope(src, ksrc, H, T, qg, qb, kg, kb, pos, 100.0, 1e-5)
+    q, k = rt.upload_f32(src), rt.upload_f32(ksrc)
+    rt.qk_norm_rope_f32_da3_base(q, k, rt.upload_f32(qg), rt.upload_f32(qb), rt.upload_f32(kg),
+                                 rt.upload_f32(kb), rt.upload_f32(pos.astype(np.float32)), H, T,
+                                 100.0, 1e-5)
+    for got, exp in ((rt.download_f32(q), eq), (rt.download_f32(k), ek)):
+        err = np.abs(got - exp)
+        assert err.mean() <= 5e-5 and err.max() <= 5e-4
+
+
+# ---- Q8_0 (bit-exact) -------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,k", [(865, 768), (3, 32), (8, 64)])
+def test_quantize_q8_0_bit_exact(rt, rows, k):
+    x = seeded.normal(81 + rows, rows * k)
+    x[:32] = 0.0  # an all-zero block: d = 0, inv = 0
+    x[32:64] *= 1e-6  # tiny scales: f16 subnormal d
+    exp = O.quantize_rows_q8_0(x, rows, k)
+    got = rt.q8_0_download(rt.quantize_q8_0(rt.upload_f32(x), rows, k))
+    assert np.array_equal(got["d"], exp["d"])
+    assert np.array_equal(got["qs"], exp["qs"])
+
+
+@pytest.mark.parametrize("m,n,k", [(865, 3072, 768), (8, 8, 64), (5, 17, 96)])
+def test_gemm_q8_0_bit_exact(rt, m, n, k):
+    """BASELINE config 4 (fc1 weights N(0, 0.02^2), activations N(0,1) quantised
+    on the device) and the tests/q8_0_dot_matches_f32.rs shape."""
+    x = seeded.normal(91, m * k)
+    w = seeded.normal(92, k * n, 0.02)
+    wt = np.ascontiguousarray(w.reshape(k, n).T).reshape(-1)
+    bq = O.quantize_rows_q8_0(wt, n, k)
+    aq = O.quantize_rows_q8_0(x, m, k)
+    exp = O.gemm_q8_0(aq, bq, m, n, k, impl="kernels")
+    a_dev = rt.quantize_q8_0(rt.upload_f32(x), m, k)
+    b_dev = rt.q8_0_upload(bq, n, k)
+    got = rt.download_f32(rt.gemm_q8_0(a_dev, b_dev, m, n, k))
+    assert_bits_equal(got, exp, "Q8_0 GEMM")

@@ -1,0 +1,124 @@
+// Device helpers shared by the gfx950 kernels: MFMA wrappers, wave64
+// reductions and explicitly rounded float ops.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vh {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// v_mfma_f32_16x16x4_f32.  Lane l supplies A[l%16][l/16] and B[l/16][l%16];
+// D[4*(l/16)+r][l%16] lands in register r of lane l.
+__device__ __forceinline__ f32x4 mfma16x16x4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// v_mfma_i32_16x16x32_i8.  Lane l supplies 8 int8 of A row l%16 at
+// k = 8*(l/16)..+7 and 8 int8 of B column l%16 at the same k;
+// D[4*(l/16)+r][l%16] lands in register r of lane l.
+__device__ __forceinline__ i32x4 mfma16x16x32_i8(long a, long b, i32x4 c) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
+
+// Separately rounded float ops: the epilogues restate reference arithmetic
+// that Rust never contracts into FMAs.  The operations are created under
+// `fp contract(off)`, so they carry no contraction flag and the backend
+// cannot fuse a multiply feeding an add even after inlining (HIP's own
+// __fmul_rn/__fadd_rn are plain operators and do get fused).
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a - b;
+}
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+__device__ __forceinline__ float div_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return __fdiv_rn(a, b);
+}
+// Correctly rounded square root.  The f32 sqrt of the device libm is only
+// faithful (1 ulp); the f64 square root rounded to f32 is exact because
+// 53 >= 2*24 + 2 makes double rounding innocuous for sqrt.
+__device__ __forceinline__ float sqrt_rn(float x) { return (float)__builtin_sqrt((double)x); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Cephes-style exp with the constants and FMA placement of the reference's
+// AVX-512 exp (src/simd_avx512.rs:22-69).  x86 min/max select the second
+// operand on NaN; cvttps truncates toward zero.
+__device__ __forceinline__ float cephes_exp(float x) {
+    x = (x < 88.37626f) ? x : 88.37626f;
+    x = (x > -88.37626f) ? x : -88.37626f;
+    float fx0 = __fmaf_rn(x, 1.44269504f, 0.5f);
+    float tr = (float)(int)fx0;
+    float fx = (tr > fx0) ? sub_rn(tr, 1.0f) : tr;
+    x = __fmaf_rn(-fx, 0.693359375f, x);
+    x = __fmaf_rn(-fx, -2.1219444e-4f, x);
+    float z = mul_rn(x, x);
+    float y = 1.98756915e-4f;
+    y = __fmaf_rn(y, x, 1.39819995e-3f);
+    y = __fmaf_rn(y, x, 8.3334519e-3f);
+    y = __fmaf_rn(y, x, 4.1665796e-2f);
+    y = __fmaf_rn(y, x, 1.6666665e-1f);
+    y = __fmaf_rn(y, x, 5.0000001e-1f);
+    y = __fmaf_rn(y, z, x);
+    y = add_rn(y, 1.0f);
+    int e = ((int)fx + 0x7f) << 23;
+    return mul_rn(y, __int_as_float(e));
+}
+
+// GELU with the AVX-512 erf of src/simd_avx512.rs:141-209:
+// t = 1/fma(c,|a|,1); Horner by FMA; y = 1 - poly*exp(-a^2) fused.
+__device__ __forceinline__ float gelu_avx512_form(float v) {
+    float a = mul_rn(v, 0.70710678f);
+    float xa = fabsf(a);
+    float sign = (a < 0.0f) ? -1.0f : 1.0f;
+    float t = div_rn(1.0f, __fmaf_rn(0.3275911f, xa, 1.0f));
+    float poly = 1.0614054f;
+    poly = __fmaf_rn(poly, t, -1.4531520f);
+    poly = __fmaf_rn(poly, t, 1.4214137f);
+    poly = __fmaf_rn(poly, t, -0.28449674f);
+    poly = __fmaf_rn(poly, t, 0.25482959f);
+    poly = mul_rn(poly, t);
+    float e = cephes_exp(sub_rn(0.0f, mul_rn(xa, xa)));
+    float y = __fmaf_rn(-poly, e, 1.0f);
+    float erf = mul_rn(sign, y);
+    return mul_rn(mul_rn(0.5f, v), add_rn(1.0f, erf));
+}
+
+// Scalar GELU of src/scalar.rs:116-134 (used by the AVX-512 path's n%16
+// tail); expf is the device libm's, within 1 ulp of glibc's.
+__device__ __forceinline__ float gelu_scalar_form(float v) {
+    float x = mul_rn(v, 0.70710677f);
+    float s = isnan(x) ? x : copysignf(1.0f, x);
+    float ax = fabsf(x);
+    float t = div_rn(1.0f, add_rn(1.0f, mul_rn(0.3275911f, ax)));
+    float p = sub_rn(mul_rn(1.0614054f, t), 1.453152f);
+    p = add_rn(mul_rn(p, t), 1.4214137f);
+    p = sub_rn(mul_rn(p, t), 0.28449674f);
+    p = add_rn(mul_rn(p, t), 0.2548296f);
+    float y = sub_rn(1.0f, mul_rn(mul_rn(p, t), expf(mul_rn(-ax, ax))));
+    return mul_rn(mul_rn(0.5f, v), add_rn(1.0f, mul_rn(s, y)));
+}
+
+}  // namespace vh

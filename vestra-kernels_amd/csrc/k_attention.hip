@@ -1,0 +1,236 @@
+// Online-softmax attention for gfx950.
+//
+// flash_kernel: DA3 head_dim 64, scale 1/8, fp32 MFMA.  A workgroup of four
+// wave64s owns 64 queries of one (image, head); wave w owns queries
+// q0+16w..q0+16w+15.  Key/value panels of 64 keys stream through LDS
+// (double-buffered, rows padded to 68 floats).  Per panel each wave computes
+//     S^T[key][query] = K[key][:] . Q[query][:]     (v_mfma_f32_16x16x4_f32)
+// so that register r of lane l holds key 16g+4(l/16)+r of query l%16 --
+// exactly the B-operand layout of the second contraction
+//     O^T[d][query] += V^T[d][key] . P^T[key][query]
+// and no register transpose or LDS round trip of P is needed.  The running
+// max and sum live in registers; a query's 64 keys are spread over the four
+// 16-lane groups, so the max takes two cross-group shuffles per panel and
+// the sum is reduced once at the end.  Exponentials run in base 2 with the
+// 1/8 * log2(e) scale folded into one multiply.
+//
+// attention_online_kernel: the reference device kernel's contract
+// (src/cuda.rs:153-194): any head_dim <= 64, one thread per (head, query).
+#include "common.h"
+#include "kernels.h"
+
+namespace vh {
+namespace {
+
+constexpr int D = 64;
+constexpr int BQ = 64;
+constexpr int BKV = 64;
+constexpr int LDP = D + 4;  // padded LDS row of a K/V panel
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <bool TOKEN_MAJOR>
+__global__ __launch_bounds__(256) void flash_kernel(const float *__restrict__ Q,
+                                                    const float *__restrict__ K,
+                                                    const float *__restrict__ V,
+                                                    float *__restrict__ O, int T, int heads) {
+    __shared__ __attribute__((aligned(16))) float Ks[2][BKV * LDP];
+    __shared__ __attribute__((aligned(16))) float Vs[2][BKV * LDP];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lh = lane >> 4;
+    const int bh = blockIdx.y;
+    const int q0 = blockIdx.x * BQ;
+    const size_t head_off = (size_t)bh * T * D;
+    const float *Qh = Q + head_off;
+    const float *Kh = K + head_off;
+    const float *Vh = V + head_off;
+
+    // This lane's query (column of S^T) and its Q fragment for all 64 dims:
+    // qf[c][s] = Q[query][16c + 4*lh + s].
+    const int query = q0 + wave * 16 + li;
+    f32x4 qf[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        qf[c] = query < T ? *reinterpret_cast<const f32x4 *>(Qh + (size_t)query * D + 16 * c + 4 * lh)
+                          : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Panel staging: 64 keys x 16 float4 = 1024 chunks, 4 per thread.
+    f32x4 rk[4], rv[4];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int c = tid + i * 256, key = c >> 4, d4 = (c & 15) * 4;
+            int gk = k0 + key;
+            if (gk < T) {
+                rk[i] = *reinterpret_cast<const f32x4 *>(Kh + (size_t)gk * D + d4);
+                rv[i] = *reinterpret_cast<const f32x4 *>(Vh + (size_t)gk * D + d4);
+            } else {
+                rk[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                rv[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int c = tid + i * 256, key = c >> 4, d4 = (c & 15) * 4;
+            *reinterpret_cast<f32x4 *>(&Ks[buf][key * LDP + d4]) = rk[i];
+            *reinterpret_cast<f32x4 *>(&Vs[buf][key * LDP + d4]) = rv[i];
+        }
+    };
+
+    const float scale = 0.125f * kLog2e;
+    float m = -INFINITY;  // running max (base-2 domain) of this lane's query
+    float l = 0.0f;       // partial running sum over this lane's keys
+    f32x4 o[4];           // o[df][r] = O[query][16*df + 4*lh + r] (unnormalised)
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int panels = (T + BKV - 1) / BKV;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int p = 0; p < panels; p++) {
+        const int cur = p & 1;
+        const int k0 = p * BKV;
+        const bool next = p + 1 < panels;
+        if (next) gload(k0 + BKV);
+
+        const float *ks = Ks[cur];
+        const float *vs = Vs[cur];
+        // S^T fragments: s[g][r] = S[key 16g+4lh+r][query li].
+        f32x4 s[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            s[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                f32x4 a = *reinterpret_cast<const f32x4 *>(&ks[(16 * g + li) * LDP + 16 * c + 4 * lh]);
+#pragma unroll
+                for (int st = 0; st < 4; st++) s[g] = mfma16x16x4(a[st], qf[c][st], s[g]);
+            }
+        }
+        // Online softmax for this lane's query over its 16 keys of the panel.
+        float mx = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int key = k0 + 16 * g + 4 * lh + r;
+                float t = key < T ? s[g][r] * scale : -INFINITY;
+                s[g][r] = t;
+                mx = fmaxf(mx, t);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(m, mx);
+        const float corr = __builtin_amdgcn_exp2f(m - mnew);
+        float psum = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float pv = __builtin_amdgcn_exp2f(s[g][r] - mnew);
+                s[g][r] = pv;
+                psum += pv;
+            }
+        l = l * corr + psum;
+        m = mnew;
+#pragma unroll
+        for (int df = 0; df < 4; df++) o[df] *= corr;
+        // O^T[d][query] += V^T[d][key] P^T[key][query]: lane supplies
+        // V[16g+4lh+st][16df+li] (A) and s[g][st] (B).
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const float *vrow = vs + (16 * g + 4 * lh + st) * LDP + li;
+#pragma unroll
+                for (int df = 0; df < 4; df++) o[df] = mfma16x16x4(vrow[16 * df], s[g][st], o[df]);
+            }
+
+        if (next) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (query >= T) return;
+    const float inv = 1.0f / l;
+    float *orow;
+    if constexpr (TOKEN_MAJOR) {
+        const int img = bh / heads, head = bh % heads;
+        orow = O + ((size_t)img * T + query) * ((size_t)heads * D) + (size_t)head * D;
+    } else {
+        orow = O + head_off + (size_t)query * D;
+    }
+#pragma unroll
+    for (int df = 0; df < 4; df++)
+        *reinterpret_cast<f32x4 *>(orow + 16 * df + 4 * lh) = o[df] * inv;
+}
+
+// src/cuda.rs:153-194 contract: one thread per (head, query), 64-key tiles.
+__global__ void attention_online_kernel(const float *__restrict__ q, const float *__restrict__ k,
+                                        const float *__restrict__ v, float *__restrict__ out,
+                                        int tokens, int hd, float scale, int rows) {
+    int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const int head = row / tokens, query = row % tokens;
+    const size_t base = (size_t)head * tokens * hd;
+    const float *qi = q + base + (size_t)query * hd;
+    float acc[64];
+    for (int d = 0; d < 64; d++) acc[d] = 0.0f;
+    float mrun = -INFINITY, lsum = 0.0f;
+    for (int j0 = 0; j0 < tokens; j0 += 64) {
+        int j1 = min(j0 + 64, tokens);
+        float sc[64];
+        float tmax = -INFINITY;
+        for (int j = j0; j < j1; j++) {
+            const float *kj = k + base + (size_t)j * hd;
+            float dot = 0.0f;
+            for (int d = 0; d < hd; d++) dot += qi[d] * kj[d];
+            sc[j - j0] = dot * scale;
+            tmax = fmaxf(tmax, sc[j - j0]);
+        }
+        float mnew = fmaxf(mrun, tmax);
+        float corr = isfinite(mrun) ? expf(mrun - mnew) : 0.0f;
+        lsum *= corr;
+        for (int d = 0; d < hd; d++) acc[d] *= corr;
+        for (int j = j0; j < j1; j++) {
+            float pv = expf(sc[j - j0] - mnew);
+            lsum += pv;
+            const float *vj = v + base + (size_t)j * hd;
+            for (int d = 0; d < hd; d++) acc[d] += pv * vj[d];
+        }
+        mrun = mnew;
+    }
+    float *oi = out + base + (size_t)query * hd;
+    float inv = 1.0f / lsum;
+    for (int d = 0; d < hd; d++) oi[d] = acc[d] * inv;
+}
+
+}  // namespace
+
+hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k, const float *v,
+                                  float *out, size_t bh, size_t tokens, size_t heads,
+                                  bool token_major) {
+    if (bh == 0 || tokens == 0) return hipSuccess;
+    dim3 grid((unsigned)((tokens + BQ - 1) / BQ), (unsigned)bh);
+    if (token_major)
+        flash_kernel<true><<<grid, 256, 0, s>>>(q, k, v, out, (int)tokens, (int)heads);
+    else
+        flash_kernel<false><<<grid, 256, 0, s>>>(q, k, v, out, (int)tokens, (int)heads);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_online(hipStream_t s, const float *q, const float *k,
+                                   const float *v, float *out, size_t heads, size_t tokens,
+                                   size_t head_dim, float scale) {
+    size_t rows = heads * tokens;
+    if (rows == 0) return hipSuccess;
+    attention_online_kernel<<<(unsigned)((rows + 63) / 64), 64, 0, s>>>(
+        q, k, v, out, (int)tokens, (int)head_dim, scale, (int)rows);
+    return hipGetLastError();
+}
+
+}  // namespace vh

@@ -1,0 +1,84 @@
+// Host-side launchers of the gfx950 kernels.  Shapes are validated by the
+// C ABI layer (runtime.hip) before any of these is called; each launcher
+// only maps a validated shape onto a grid and returns the launch status.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace vh {
+
+// ---- elementwise / layout (k_elementwise.hip) ----------------------------
+hipError_t launch_add(hipStream_t s, float *dst, const float *src, size_t n);
+hipError_t launch_bias_scale(hipStream_t s, float *v, const float *bias, const float *gamma,
+                             size_t rows, size_t cols);
+hipError_t launch_gelu(hipStream_t s, float *v, size_t n);
+hipError_t launch_layernorm(hipStream_t s, const float *in, const float *gamma,
+                            const float *beta, float *out, size_t rows, size_t cols, float eps);
+hipError_t launch_layernorm_cpu_order(hipStream_t s, const float *in, const float *gamma,
+                                      const float *beta, float *out, size_t rows, size_t cols,
+                                      float eps);
+hipError_t launch_split_qkv(hipStream_t s, const float *qkv, float *q, float *k, float *v,
+                            size_t tokens, size_t heads, size_t head_dim);
+hipError_t launch_hnd_to_token(hipStream_t s, const float *hnd, float *out, size_t tokens,
+                               size_t heads, size_t head_dim);
+hipError_t launch_token_to_chw(hipStream_t s, const float *tm, float *chw, size_t tokens,
+                               size_t channels);
+hipError_t launch_patchify(hipStream_t s, const float *image, float *patches, size_t height,
+                           size_t width, size_t patch, size_t channels);
+hipError_t launch_prepend_cls_add_pos(hipStream_t s, const float *patches, const float *cls,
+                                      const float *pos, float *out, size_t patch_count,
+                                      size_t embed);
+// rot: [n][2][head_dim/4][sin, cos]
+hipError_t launch_rope2d(hipStream_t s, float *x, size_t heads, size_t n, size_t head_dim,
+                         const float *rot);
+// rot: [tokens][2][16][sin, cos]; rows = heads*tokens rows of 64
+hipError_t launch_qk_norm_rope(hipStream_t s, float *q, float *k, const float *qg,
+                               const float *qb, const float *kg, const float *kb,
+                               const float *rot, size_t rows, size_t tokens, float eps);
+// Table for qk_norm_rope from device f32 positions [tokens][2].
+hipError_t launch_rope_table_device(hipStream_t s, const float *pos, size_t tokens, float freq,
+                                    float *rot);
+hipError_t launch_transpose(hipStream_t s, const float *in, float *out, size_t rows,
+                            size_t cols);
+
+// ---- attention (k_attention.hip) ----------------------------------------
+// Generic online softmax for head_dim <= 64 (the reference device oracle's
+// contract), one thread per (head, query).
+hipError_t launch_attention_online(hipStream_t s, const float *q, const float *k,
+                                   const float *v, float *out, size_t heads, size_t tokens,
+                                   size_t head_dim, float scale);
+// fp32-MFMA flash attention, head_dim 64, scale 1/8.  q/k/v [bh][tokens][64]
+// with bh = images*heads; out head-major or token-major [img][tokens][heads*64].
+hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k, const float *v,
+                                  float *out, size_t bh, size_t tokens, size_t heads,
+                                  bool token_major);
+
+// ---- GEMM (k_gemm.hip) ----------------------------------------------------
+enum class Epi : int { Store = 0, Gelu = 1, Residual = 2, Qkv = 3 };
+
+struct GemmArgs {
+    const float *a;  // [m][k] row-major
+    const float *bt; // [n][k] row-major (weights pre-transposed)
+    size_t m, n, k;
+    Epi epi;
+    float *c;            // Store / Gelu / Residual: [m][n]
+    const float *bias;   // [n] or null
+    const float *gamma;  // [n] or null (Store, Residual)
+    // Qkv: outputs [images][heads][tokens][64]; rot [tokens][2][16][2] or null
+    float *q, *k_out, *v;
+    size_t tokens, heads;
+    const float *rot;
+};
+hipError_t launch_gemm(hipStream_t s, const GemmArgs &g);
+
+// ---- Q8_0 (k_q8.hip) --------------------------------------------------------
+// x [rows][k] -> qs [rows][k] int8, d [rows][k/32] f16 bits
+hipError_t launch_quantize_q8_0(hipStream_t s, const float *x, int8_t *qs, uint16_t *d,
+                                size_t rows, size_t k);
+hipError_t launch_gemm_q8_0(hipStream_t s, const int8_t *a_qs, const uint16_t *a_d,
+                            const int8_t *b_qs, const uint16_t *b_d, float *c, size_t m,
+                            size_t n, size_t k);
+
+}  // namespace vh

@@ -1,0 +1,1558 @@
+// C ABI of the MI355X backend (include/vestra_hip.h): runtime, tensors,
+// prepared projections, Q8_0 tensors and the DA3-BASE block driver.
+//
+// Each entry point validates every argument before touching HIP, maps HIP
+// failures onto the CudaError-shaped status codes and records a thread-local
+// message.  Device memory comes from the stream-ordered pool of the
+// runtime's device (hipMallocAsync / hipFreeAsync on the runtime stream), so
+// chained operators never synchronise and never upload zero-filled buffers
+// from the host.
+#include "../../include/vestra_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+thread_local size_t g_mm_dst = 0, g_mm_src = 0;
+
+vh_status fail(vh_status st, const std::string &msg) {
+    g_err = msg;
+    return st;
+}
+
+vh_status mismatch(size_t dst, size_t src, const char *what) {
+    g_mm_dst = dst;
+    g_mm_src = src;
+    return fail(VH_ERR_LENGTH_MISMATCH, std::string(what) + ": length mismatch, destination " +
+                                            std::to_string(dst) + ", source " +
+                                            std::to_string(src));
+}
+
+vh_status null_arg(const char *what) {
+    return fail(VH_ERR_INVALID_ARGUMENT, std::string(what) + ": null handle or pointer");
+}
+
+std::string hip_msg(const char *what, hipError_t e) {
+    return std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+}
+
+struct ProfileRec {
+    const char *name;
+    hipEvent_t a, b;
+};
+
+struct RtState {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+    std::map<std::string, float *> rope_cache;  // host-built sin/cos tables
+    float *ws = nullptr;                        // grow-only block workspace
+    size_t ws_floats = 0;
+    bool profile = false;
+    std::vector<ProfileRec> pending;
+    std::map<std::string, std::pair<unsigned long long, double>> totals;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+
+    ~RtState() {
+        if (!stream) return;
+        hipSetDevice(device);
+        hipStreamSynchronize(stream);
+        for (auto &kv : rope_cache) hipFree(kv.second);
+        if (ws) hipFree(ws);
+        for (auto &p : pending) {
+            hipEventDestroy(p.a);
+            hipEventDestroy(p.b);
+        }
+        if (t0) hipEventDestroy(t0);
+        if (t1) hipEventDestroy(t1);
+        hipStreamDestroy(stream);
+    }
+};
+
+using Rt = std::shared_ptr<RtState>;
+
+}  // namespace
+
+struct vh_runtime {
+    Rt s;
+};
+
+struct vh_tensor {
+    Rt rt;
+    float *ptr = nullptr;
+    size_t len = 0;
+    ~vh_tensor() {
+        if (ptr && rt) {
+            hipSetDevice(rt->device);
+            hipFreeAsync(ptr, rt->stream);
+        }
+    }
+};
+
+namespace {
+
+struct Lin {
+    size_t K = 0, N = 0;
+    float *wt = nullptr;  // [N][K]
+    float *bias = nullptr;
+    float *gamma = nullptr;  // null = unit LayerScale
+};
+
+}  // namespace
+
+struct vh_linear {
+    Rt rt;
+    Lin L;
+    ~vh_linear() {
+        if (!rt) return;
+        hipSetDevice(rt->device);
+        for (float *p : {L.wt, L.bias, L.gamma})
+            if (p) hipFreeAsync(p, rt->stream);
+    }
+};
+
+struct vh_q8_tensor {
+    Rt rt;
+    size_t rows = 0, k = 0;
+    int8_t *qs = nullptr;
+    uint16_t *d = nullptr;
+    ~vh_q8_tensor() {
+        if (!rt) return;
+        hipSetDevice(rt->device);
+        if (qs) hipFreeAsync(qs, rt->stream);
+        if (d) hipFreeAsync(d, rt->stream);
+    }
+};
+
+struct vh_block {
+    Rt rt;
+    Lin qkv, proj, fc1, fc2;
+    float *ln1_g = nullptr, *ln1_b = nullptr, *ln2_g = nullptr, *ln2_b = nullptr;
+    ~vh_block() {
+        if (!rt) return;
+        hipSetDevice(rt->device);
+        for (Lin *l : {&qkv, &proj, &fc1, &fc2})
+            for (float *p : {l->wt, l->bias, l->gamma})
+                if (p) hipFreeAsync(p, rt->stream);
+        for (float *p : {ln1_g, ln1_b, ln2_g, ln2_b})
+            if (p) hipFreeAsync(p, rt->stream);
+    }
+};
+
+namespace {
+
+// ---- device helpers ----------------------------------------------------------
+
+vh_status set_device(RtState &s) {
+    hipError_t e = hipSetDevice(s.device);
+    if (e != hipSuccess) return fail(VH_ERR_KERNEL, hip_msg("hipSetDevice", e));
+    return VH_OK;
+}
+
+template <class T>
+vh_status dalloc(RtState &s, size_t count, T **out, const char *what) {
+    size_t bytes = (count ? count : 1) * sizeof(T);
+    void *p = nullptr;
+    hipError_t e = hipMallocAsync(&p, bytes, s.stream);
+    if (e != hipSuccess) return fail(VH_ERR_UPLOAD, hip_msg(what, e));
+    *out = static_cast<T *>(p);
+    return VH_OK;
+}
+
+vh_status h2d(RtState &s, void *dst, const void *src, size_t bytes, const char *what) {
+    if (bytes == 0) return VH_OK;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s.stream);  // host buffer reusable on return
+    if (e != hipSuccess) return fail(VH_ERR_UPLOAD, hip_msg(what, e));
+    return VH_OK;
+}
+
+vh_status upload_array(RtState &s, const float *host, size_t n, float **out, const char *what) {
+    vh_status st = dalloc(s, n, out, what);
+    if (st) return st;
+    st = h2d(s, *out, host, n * sizeof(float), what);
+    if (st) {
+        hipFreeAsync(*out, s.stream);
+        *out = nullptr;
+    }
+    return st;
+}
+
+vh_status new_tensor(const Rt &rt, size_t len, vh_tensor **out, const char *what) {
+    float *p = nullptr;
+    vh_status st = dalloc(*rt, len, &p, what);
+    if (st) return st;
+    vh_tensor *t = new (std::nothrow) vh_tensor;
+    if (!t) {
+        hipFreeAsync(p, rt->stream);
+        return fail(VH_ERR_UPLOAD, std::string(what) + ": host allocation failed");
+    }
+    t->rt = rt;
+    t->ptr = p;
+    t->len = len;
+    *out = t;
+    return VH_OK;
+}
+
+// Runs a launcher, bracketing it with profiling events when enabled.
+template <class F>
+vh_status launch(RtState &s, const char *name, F &&f) {
+    hipEvent_t a = nullptr, b = nullptr;
+    if (s.profile) {
+        hipEventCreate(&a);
+        hipEventCreate(&b);
+        hipEventRecord(a, s.stream);
+    }
+    hipError_t e = f();
+    if (s.profile) {
+        hipEventRecord(b, s.stream);
+        s.pending.push_back({name, a, b});
+    }
+    if (e != hipSuccess) return fail(VH_ERR_KERNEL, hip_msg(name, e));
+    return VH_OK;
+}
+
+// rope::rope2d / rope_rotations tables (src/rope.rs:42-60,
+// src/specialized.rs:389-410), built on the host with the platform libm the
+// reference calls and cached per (positions, head_dim, frequency).
+vh_status rope_table(RtState &s, const int64_t *pos, size_t n, size_t head_dim, float freq,
+                     const float **out) {
+    const size_t half = head_dim / 2, quarter = half / 2;
+    std::string key;
+    key.append(reinterpret_cast<const char *>(&freq), sizeof(freq));
+    key.append(reinterpret_cast<const char *>(&head_dim), sizeof(head_dim));
+    key.append(reinterpret_cast<const char *>(pos), n * 2 * sizeof(int64_t));
+    std::lock_guard<std::mutex> lock(s.mu);
+    auto it = s.rope_cache.find(key);
+    if (it != s.rope_cache.end()) {
+        *out = it->second;
+        return VH_OK;
+    }
+    std::vector<float> inv(quarter);
+    for (size_t i = 0; i < quarter; i++) inv[i] = powf(freq, -2.0f * (float)i / (float)half);
+    std::vector<float> rot(n * 2 * quarter * 2);
+    for (size_t p = 0; p < n; p++)
+        for (size_t axis = 0; axis < 2; axis++) {
+            const float position = (float)pos[2 * p + axis];
+            for (size_t i = 0; i < quarter; i++) {
+                const float arg = position * inv[i];
+                const size_t o = ((p * 2 + axis) * quarter + i) * 2;
+                rot[o] = sinf(arg);
+                rot[o + 1] = cosf(arg);
+            }
+        }
+    float *d = nullptr;
+    hipError_t e = hipMalloc(&d, rot.size() * sizeof(float));
+    if (e != hipSuccess) return fail(VH_ERR_UPLOAD, hip_msg("RoPE table allocation", e));
+    e = hipMemcpy(d, rot.data(), rot.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        hipFree(d);
+        return fail(VH_ERR_UPLOAD, hip_msg("RoPE table upload", e));
+    }
+    s.rope_cache.emplace(key, d);
+    *out = d;
+    return VH_OK;
+}
+
+vh_status workspace(RtState &s, size_t floats, float **out) {
+    if (s.ws_floats < floats) {
+        hipStreamSynchronize(s.stream);
+        if (s.ws) hipFree(s.ws);
+        s.ws = nullptr;
+        s.ws_floats = 0;
+        hipError_t e = hipMalloc(&s.ws, floats * sizeof(float));
+        if (e != hipSuccess) return fail(VH_ERR_UPLOAD, hip_msg("block workspace allocation", e));
+        s.ws_floats = floats;
+    }
+    *out = s.ws;
+    return VH_OK;
+}
+
+vh_status prepare_lin(RtState &s, size_t K, size_t N, const float *w, const float *bias,
+                      const float *gamma, Lin *L) {
+    float *tmp = nullptr;
+    vh_status st = upload_array(s, w, K * N, &tmp, "linear weight upload");
+    if (st) return st;
+    st = dalloc(s, K * N, &L->wt, "linear weight allocation");
+    if (!st)
+        st = launch(s, "transpose_weight", [&] { return vh::launch_transpose(s.stream, tmp, L->wt, K, N); });
+    hipFreeAsync(tmp, s.stream);
+    if (!st) st = upload_array(s, bias, N, &L->bias, "linear bias upload");
+    if (!st && gamma) st = upload_array(s, gamma, N, &L->gamma, "linear gamma upload");
+    if (st) {
+        for (float *p : {L->wt, L->bias, L->gamma})
+            if (p) hipFreeAsync(p, s.stream);
+        *L = Lin{};
+        return st;
+    }
+    L->K = K;
+    L->N = N;
+    return VH_OK;
+}
+
+vh_status run_lin(RtState &s, const Lin &L, const float *in, size_t rows, vh::Epi epi, float *c,
+                  const char *name) {
+    vh::GemmArgs g{};
+    g.a = in;
+    g.bt = L.wt;
+    g.m = rows;
+    g.n = L.N;
+    g.k = L.K;
+    g.epi = epi;
+    g.c = c;
+    g.bias = L.bias;
+    g.gamma = epi == vh::Epi::Gelu ? nullptr : L.gamma;
+    return launch(s, name, [&] { return vh::launch_gemm(s.stream, g); });
+}
+
+vh_status run_qkv(RtState &s, const Lin &L, const float *in, size_t images, size_t tokens,
+                  size_t heads, const float *rot, float *q, float *k, float *v) {
+    vh::GemmArgs g{};
+    g.a = in;
+    g.bt = L.wt;
+    g.m = images * tokens;
+    g.n = L.N;
+    g.k = L.K;
+    g.epi = vh::Epi::Qkv;
+    g.bias = L.bias;
+    g.q = q;
+    g.k_out = k;
+    g.v = v;
+    g.tokens = tokens;
+    g.heads = heads;
+    g.rot = rot;
+    return launch(s, "gemm_qkv_rope", [&] { return vh::launch_gemm(s.stream, g); });
+}
+
+#define NEED(p, what) \
+    do {              \
+        if (!(p)) return null_arg(what); \
+    } while (0)
+
+#define TRY(expr)                   \
+    do {                            \
+        vh_status st_ = (expr);     \
+        if (st_ != VH_OK) return st_; \
+    } while (0)
+
+#define GUARD_BEGIN try {
+#define GUARD_END                                                              \
+    }                                                                          \
+    catch (const std::bad_alloc &) {                                           \
+        return fail(VH_ERR_UPLOAD, "host allocation failed");                 \
+    }                                                                          \
+    catch (...) {                                                              \
+        return fail(VH_ERR_KERNEL, "unexpected host exception");             \
+    }
+
+bool mul_overflows(size_t a, size_t b, size_t *out) { return __builtin_mul_overflow(a, b, out); }
+
+}  // namespace
+
+// =============================================================================
+// errors
+// =============================================================================
+
+extern "C" const char *vh_last_error(void) { return g_err.c_str(); }
+
+extern "C" void vh_last_length_mismatch(size_t *destination, size_t *source_len) {
+    if (destination) *destination = g_mm_dst;
+    if (source_len) *source_len = g_mm_src;
+}
+
+// =============================================================================
+// runtime
+// =============================================================================
+
+extern "C" vh_status vh_runtime_new(size_t device, vh_runtime **out) {
+    NEED(out, "vh_runtime_new");
+    GUARD_BEGIN
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0)
+        return fail(VH_ERR_INITIALIZE, "failed to initialize HIP device " + std::to_string(device) +
+                                           ": no HIP device (" + hipGetErrorString(e) + ")");
+    if (device >= (size_t)count)
+        return fail(VH_ERR_INITIALIZE, "failed to initialize HIP device " + std::to_string(device) +
+                                           ": only " + std::to_string(count) + " device(s)");
+    auto s = std::make_shared<RtState>();
+    s->device = (int)device;
+    e = hipSetDevice(s->device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
+    if (e != hipSuccess)
+        return fail(VH_ERR_INITIALIZE, "failed to initialize HIP device " + std::to_string(device) +
+                                           ": " + hipGetErrorString(e));
+    // Keep freed blocks in the stream-ordered pool instead of returning them
+    // to the driver at every synchronisation.
+    hipMemPool_t pool = nullptr;
+    if (hipDeviceGetDefaultMemPool(&pool, s->device) == hipSuccess && pool) {
+        uint64_t threshold = UINT64_MAX;
+        hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &threshold);
+    }
+    vh_runtime *rt = new vh_runtime;
+    rt->s = s;
+    *out = rt;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_runtime_clone(const vh_runtime *rt, vh_runtime **out) {
+    NEED(rt, "vh_runtime_clone");
+    NEED(out, "vh_runtime_clone");
+    GUARD_BEGIN
+    vh_runtime *c = new vh_runtime;
+    c->s = rt->s;
+    *out = c;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" void vh_runtime_free(vh_runtime *rt) { delete rt; }
+
+extern "C" size_t vh_runtime_device(const vh_runtime *rt) { return rt ? (size_t)rt->s->device : 0; }
+
+extern "C" void *vh_runtime_stream(const vh_runtime *rt) {
+    return rt ? (void *)rt->s->stream : nullptr;
+}
+
+extern "C" vh_status vh_runtime_synchronize(const vh_runtime *rt) {
+    NEED(rt, "vh_runtime_synchronize");
+    TRY(set_device(*rt->s));
+    hipError_t e = hipStreamSynchronize(rt->s->stream);
+    if (e != hipSuccess) return fail(VH_ERR_KERNEL, hip_msg("stream synchronize", e));
+    return VH_OK;
+}
+
+// =============================================================================
+// tensors
+// =============================================================================
+
+extern "C" vh_status vh_upload_f32(const vh_runtime *rt, const float *values, size_t len,
+                                   vh_tensor **out) {
+    NEED(rt, "vh_upload_f32");
+    NEED(out, "vh_upload_f32");
+    if (len && !values) return null_arg("vh_upload_f32 values");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, len, &t, "upload allocation"));
+    vh_status st = h2d(s, t->ptr, values, len * sizeof(float), "host-to-device transfer");
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_download_f32(const vh_runtime *rt, const vh_tensor *tensor, float *out,
+                                     size_t out_len) {
+    NEED(rt, "vh_download_f32");
+    NEED(tensor, "vh_download_f32");
+    if (out_len != tensor->len) return mismatch(out_len, tensor->len, "vh_download_f32");
+    if (out_len && !out) return null_arg("vh_download_f32 out");
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    if (out_len == 0) return VH_OK;
+    hipError_t e = hipMemcpyAsync(out, tensor->ptr, out_len * sizeof(float),
+                                  hipMemcpyDeviceToHost, s.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s.stream);
+    if (e != hipSuccess) return fail(VH_ERR_DOWNLOAD, hip_msg("device-to-host transfer", e));
+    return VH_OK;
+}
+
+extern "C" vh_status vh_tensor_alloc(const vh_runtime *rt, size_t len, vh_tensor **out) {
+    NEED(rt, "vh_tensor_alloc");
+    NEED(out, "vh_tensor_alloc");
+    GUARD_BEGIN
+    TRY(set_device(*rt->s));
+    return new_tensor(rt->s, len, out, "tensor allocation");
+    GUARD_END
+}
+
+extern "C" void vh_tensor_free(vh_tensor *tensor) { delete tensor; }
+extern "C" size_t vh_tensor_len(const vh_tensor *tensor) { return tensor ? tensor->len : 0; }
+extern "C" int vh_tensor_is_empty(const vh_tensor *tensor) { return !tensor || tensor->len == 0; }
+extern "C" float *vh_tensor_device_ptr(const vh_tensor *tensor) {
+    return tensor ? tensor->ptr : nullptr;
+}
+
+// =============================================================================
+// copies / residual
+// =============================================================================
+
+static vh_status d2d(RtState &s, float *dst, const float *src, size_t n, const char *what) {
+    if (n == 0) return VH_OK;
+    return launch(s, what, [&] {
+        return hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyDeviceToDevice, s.stream);
+    });
+}
+
+extern "C" vh_status vh_copy_f32(const vh_runtime *rt, const vh_tensor *source, vh_tensor **out) {
+    NEED(rt, "vh_copy_f32");
+    NEED(source, "vh_copy_f32");
+    NEED(out, "vh_copy_f32");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, source->len, &t, "copy allocation"));
+    vh_status st = d2d(s, t->ptr, source->ptr, source->len, "copy");
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_copy_segment_f32(const vh_runtime *rt, const vh_tensor *source,
+                                         size_t source_offset, size_t len, vh_tensor **out) {
+    NEED(rt, "vh_copy_segment_f32");
+    NEED(source, "vh_copy_segment_f32");
+    NEED(out, "vh_copy_segment_f32");
+    size_t end = 0;
+    if (__builtin_add_overflow(source_offset, len, &end) || end > source->len)
+        return mismatch(len, source->len > source_offset ? source->len - source_offset : 0,
+                        "vh_copy_segment_f32");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, len, &t, "segment allocation"));
+    vh_status st = d2d(s, t->ptr, source->ptr + source_offset, len, "copy_segment");
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_copy_segment_into_f32(const vh_runtime *rt, vh_tensor *destination,
+                                              size_t destination_offset, const vh_tensor *source,
+                                              size_t source_offset, size_t len) {
+    NEED(rt, "vh_copy_segment_into_f32");
+    NEED(destination, "vh_copy_segment_into_f32");
+    NEED(source, "vh_copy_segment_into_f32");
+    size_t dend = 0, send = 0;
+    bool bad = __builtin_add_overflow(destination_offset, len, &dend) ||
+               __builtin_add_overflow(source_offset, len, &send) || dend > destination->len ||
+               send > source->len;
+    if (bad)
+        return mismatch(destination->len > destination_offset ? destination->len - destination_offset : 0,
+                        source->len > source_offset ? source->len - source_offset : 0,
+                        "vh_copy_segment_into_f32");
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    return d2d(s, destination->ptr + destination_offset, source->ptr + source_offset, len,
+               "copy_segment_into");
+}
+
+extern "C" vh_status vh_overwrite_prefix_f32(const vh_runtime *rt, vh_tensor *destination,
+                                             const vh_tensor *source, size_t len) {
+    NEED(rt, "vh_overwrite_prefix_f32");
+    NEED(destination, "vh_overwrite_prefix_f32");
+    NEED(source, "vh_overwrite_prefix_f32");
+    if (len > destination->len || len > source->len)
+        return mismatch(destination->len, source->len, "vh_overwrite_prefix_f32");
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    return d2d(s, destination->ptr, source->ptr, len, "overwrite_prefix");
+}
+
+extern "C" vh_status vh_add_f32_in_place(const vh_runtime *rt, vh_tensor *destination,
+                                         const vh_tensor *source) {
+    NEED(rt, "vh_add_f32_in_place");
+    NEED(destination, "vh_add_f32_in_place");
+    NEED(source, "vh_add_f32_in_place");
+    if (destination->len != source->len)
+        return mismatch(destination->len, source->len, "vh_add_f32_in_place");
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    return launch(s, "add", [&] {
+        return vh::launch_add(s.stream, destination->ptr, source->ptr, destination->len);
+    });
+}
+
+// =============================================================================
+// GEMM and epilogues
+// =============================================================================
+
+extern "C" vh_status vh_gemm_row_major_f32(const vh_runtime *rt, const vh_tensor *a,
+                                           const vh_tensor *b, size_t m, size_t k, size_t n,
+                                           vh_tensor **out) {
+    NEED(rt, "vh_gemm_row_major_f32");
+    NEED(a, "vh_gemm_row_major_f32");
+    NEED(b, "vh_gemm_row_major_f32");
+    NEED(out, "vh_gemm_row_major_f32");
+    size_t mk = 0, kn = 0, mn = 0;
+    if (mul_overflows(m, k, &mk) || mul_overflows(k, n, &kn) || mul_overflows(m, n, &mn) ||
+        a->len != mk || b->len != kn)
+        return fail(VH_ERR_BLAS, "row-major GEMM shape M=" + std::to_string(m) + ", K=" +
+                                     std::to_string(k) + ", N=" + std::to_string(n) +
+                                     " does not match A=" + std::to_string(a->len) +
+                                     " or B=" + std::to_string(b->len));
+    if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
+        return fail(VH_ERR_BLAS, "row-major GEMM dimension exceeds 2^31-1");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, mn, &t, "GEMM output allocation"));
+    float *bt = nullptr;
+    vh_status st = dalloc(s, kn, &bt, "GEMM operand allocation");
+    if (!st)
+        st = launch(s, "transpose_b", [&] { return vh::launch_transpose(s.stream, b->ptr, bt, k, n); });
+    if (!st) {
+        vh::GemmArgs g{};
+        g.a = a->ptr;
+        g.bt = bt;
+        g.m = m;
+        g.n = n;
+        g.k = k;
+        g.epi = vh::Epi::Store;
+        g.c = t->ptr;
+        st = launch(s, "gemm", [&] { return vh::launch_gemm(s.stream, g); });
+    }
+    if (bt) hipFreeAsync(bt, s.stream);
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_bias_scale_f32_in_place(const vh_runtime *rt, vh_tensor *values,
+                                                const vh_tensor *bias, const vh_tensor *gamma,
+                                                size_t rows, size_t columns) {
+    NEED(rt, "vh_bias_scale_f32_in_place");
+    NEED(values, "vh_bias_scale_f32_in_place");
+    NEED(bias, "vh_bias_scale_f32_in_place");
+    NEED(gamma, "vh_bias_scale_f32_in_place");
+    size_t expected = 0;
+    if (mul_overflows(rows, columns, &expected) || values->len != expected ||
+        bias->len != columns || gamma->len != columns)
+        return mismatch(values->len, expected, "vh_bias_scale_f32_in_place");
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    return launch(s, "bias_scale", [&] {
+        return vh::launch_bias_scale(s.stream, values->ptr, bias->ptr, gamma->ptr, rows, columns);
+    });
+}
+
+extern "C" vh_status vh_gelu_f32_in_place(const vh_runtime *rt, vh_tensor *values) {
+    NEED(rt, "vh_gelu_f32_in_place");
+    NEED(values, "vh_gelu_f32_in_place");
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    return launch(s, "gelu", [&] { return vh::launch_gelu(s.stream, values->ptr, values->len); });
+}
+
+// =============================================================================
+// LayerNorm
+// =============================================================================
+
+static vh_status layernorm_common(const vh_runtime *rt, const vh_tensor *input,
+                                  const vh_tensor *gamma, const vh_tensor *beta, size_t rows,
+                                  size_t columns, float eps, vh_tensor **out, bool cpu_order) {
+    const char *name = cpu_order ? "vh_layernorm_f32_cpu_order" : "vh_layernorm_f32";
+    NEED(rt, name);
+    NEED(input, name);
+    NEED(gamma, name);
+    NEED(beta, name);
+    NEED(out, name);
+    size_t expected = 0;
+    if (mul_overflows(rows, columns, &expected) || input->len != expected ||
+        gamma->len != columns || beta->len != columns)
+        return mismatch(input->len, expected, name);
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, expected, &t, "LayerNorm output allocation"));
+    vh_status st = launch(s, cpu_order ? "layernorm_cpu_order" : "layernorm", [&] {
+        return cpu_order ? vh::launch_layernorm_cpu_order(s.stream, input->ptr, gamma->ptr,
+                                                          beta->ptr, t->ptr, rows, columns, eps)
+                         : vh::launch_layernorm(s.stream, input->ptr, gamma->ptr, beta->ptr,
+                                                t->ptr, rows, columns, eps);
+    });
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_layernorm_f32(const vh_runtime *rt, const vh_tensor *input,
+                                      const vh_tensor *gamma, const vh_tensor *beta, size_t rows,
+                                      size_t columns, float epsilon, vh_tensor **out) {
+    return layernorm_common(rt, input, gamma, beta, rows, columns, epsilon, out, false);
+}
+
+extern "C" vh_status vh_layernorm_f32_cpu_order(const vh_runtime *rt, const vh_tensor *input,
+                                                const vh_tensor *gamma, const vh_tensor *beta,
+                                                size_t rows, size_t columns, float epsilon,
+                                                vh_tensor **out) {
+    return layernorm_common(rt, input, gamma, beta, rows, columns, epsilon, out, true);
+}
+
+// =============================================================================
+// attention
+// =============================================================================
+
+extern "C" vh_status vh_attention_online_f32(const vh_runtime *rt, const vh_tensor *q,
+                                             const vh_tensor *k, const vh_tensor *v, size_t heads,
+                                             size_t tokens, size_t head_dim, vh_tensor **out) {
+    NEED(rt, "vh_attention_online_f32");
+    NEED(q, "vh_attention_online_f32");
+    NEED(k, "vh_attention_online_f32");
+    NEED(v, "vh_attention_online_f32");
+    NEED(out, "vh_attention_online_f32");
+    if (head_dim == 0 || head_dim > 64)
+        return fail(VH_ERR_KERNEL, "online attention supports 1..=64 head dimensions, got " +
+                                       std::to_string(head_dim));
+    size_t ht = 0, expected = 0;
+    if (mul_overflows(heads, tokens, &ht) || mul_overflows(ht, head_dim, &expected) ||
+        q->len != expected || k->len != expected || v->len != expected)
+        return mismatch(q->len, expected, "vh_attention_online_f32");
+    if (tokens > INT32_MAX || ht > INT32_MAX)
+        return fail(VH_ERR_KERNEL, "attention rows exceed 2^31-1");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, expected, &t, "attention output allocation"));
+    vh_status st;
+    if (head_dim == 64) {
+        st = launch(s, "flash_attention", [&] {
+            return vh::launch_flash_attention(s.stream, q->ptr, k->ptr, v->ptr, t->ptr, heads,
+                                              tokens, heads, false);
+        });
+    } else {
+        const float scale = 1.0f / sqrtf((float)head_dim);
+        st = launch(s, "attention_online", [&] {
+            return vh::launch_attention_online(s.stream, q->ptr, k->ptr, v->ptr, t->ptr, heads,
+                                               tokens, head_dim, scale);
+        });
+    }
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_flash_attention_f32_da3_base(const vh_runtime *rt, const vh_tensor *q,
+                                                     const vh_tensor *k, const vh_tensor *v,
+                                                     size_t heads, size_t tokens, int token_major,
+                                                     vh_tensor **out) {
+    NEED(rt, "vh_flash_attention_f32_da3_base");
+    NEED(q, "vh_flash_attention_f32_da3_base");
+    NEED(k, "vh_flash_attention_f32_da3_base");
+    NEED(v, "vh_flash_attention_f32_da3_base");
+    NEED(out, "vh_flash_attention_f32_da3_base");
+    size_t ht = 0, expected = 0;
+    if (mul_overflows(heads, tokens, &ht) || mul_overflows(ht, 64, &expected) ||
+        q->len != expected || k->len != expected || v->len != expected)
+        return mismatch(q->len, expected, "vh_flash_attention_f32_da3_base");
+    if (tokens > INT32_MAX || heads > 65535)
+        return fail(VH_ERR_KERNEL, "flash attention shape exceeds the launch grid");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, expected, &t, "attention output allocation"));
+    vh_status st = launch(s, "flash_attention", [&] {
+        return vh::launch_flash_attention(s.stream, q->ptr, k->ptr, v->ptr, t->ptr, heads, tokens,
+                                          heads, token_major != 0);
+    });
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+// =============================================================================
+// layout
+// =============================================================================
+
+extern "C" vh_status vh_split_qkv_hnd_f32(const vh_runtime *rt, const vh_tensor *qkv,
+                                          size_t tokens, size_t heads, size_t head_dim,
+                                          vh_tensor **q, vh_tensor **k, vh_tensor **v) {
+    NEED(rt, "vh_split_qkv_hnd_f32");
+    NEED(qkv, "vh_split_qkv_hnd_f32");
+    NEED(q, "vh_split_qkv_hnd_f32");
+    NEED(k, "vh_split_qkv_hnd_f32");
+    NEED(v, "vh_split_qkv_hnd_f32");
+    size_t per = 0, len = 0, expected = 0;
+    if (mul_overflows(heads, head_dim, &per) || mul_overflows(tokens, per, &len) ||
+        mul_overflows(len, 3, &expected) || qkv->len != expected || per == 0)
+        return mismatch(qkv->len, expected, "vh_split_qkv_hnd_f32");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *tq = nullptr, *tk = nullptr, *tv = nullptr;
+    vh_status st = new_tensor(rt->s, len, &tq, "QKV layout output allocation");
+    if (!st) st = new_tensor(rt->s, len, &tk, "QKV layout output allocation");
+    if (!st) st = new_tensor(rt->s, len, &tv, "QKV layout output allocation");
+    if (!st)
+        st = launch(s, "split_qkv_hnd", [&] {
+            return vh::launch_split_qkv(s.stream, qkv->ptr, tq->ptr, tk->ptr, tv->ptr, tokens,
+                                        heads, head_dim);
+        });
+    if (st) {
+        delete tq;
+        delete tk;
+        delete tv;
+        return st;
+    }
+    *q = tq;
+    *k = tk;
+    *v = tv;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_hnd_to_token_f32(const vh_runtime *rt, const vh_tensor *hnd,
+                                         size_t tokens, size_t heads, size_t head_dim,
+                                         vh_tensor **out) {
+    NEED(rt, "vh_hnd_to_token_f32");
+    NEED(hnd, "vh_hnd_to_token_f32");
+    NEED(out, "vh_hnd_to_token_f32");
+    size_t per = 0, len = 0;
+    if (mul_overflows(heads, head_dim, &per) || mul_overflows(tokens, per, &len) ||
+        hnd->len != len || per == 0)
+        return mismatch(hnd->len, len, "vh_hnd_to_token_f32");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, len, &t, "attention layout output allocation"));
+    vh_status st = launch(s, "hnd_to_token", [&] {
+        return vh::launch_hnd_to_token(s.stream, hnd->ptr, t->ptr, tokens, heads, head_dim);
+    });
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_token_to_chw_f32(const vh_runtime *rt, const vh_tensor *token_major,
+                                         size_t tokens, size_t channels, vh_tensor **out) {
+    NEED(rt, "vh_token_to_chw_f32");
+    NEED(token_major, "vh_token_to_chw_f32");
+    NEED(out, "vh_token_to_chw_f32");
+    size_t len = 0;
+    if (mul_overflows(tokens, channels, &len) || token_major->len != len || tokens == 0 ||
+        channels == 0)
+        return mismatch(token_major->len, len, "vh_token_to_chw_f32");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, len, &t, "CHW allocation"));
+    vh_status st = launch(s, "token_to_chw", [&] {
+        return vh::launch_token_to_chw(s.stream, token_major->ptr, t->ptr, tokens, channels);
+    });
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_patchify_nchw_f32(const vh_runtime *rt, const vh_tensor *image,
+                                          size_t height, size_t width, size_t patch,
+                                          size_t channels, vh_tensor **out) {
+    NEED(rt, "vh_patchify_nchw_f32");
+    NEED(image, "vh_patchify_nchw_f32");
+    NEED(out, "vh_patchify_nchw_f32");
+    size_t hw = 0, chw = 0;
+    bool bad = height == 0 || width == 0 || patch == 0 || channels == 0 ||
+               height % patch != 0 || width % patch != 0 || mul_overflows(height, width, &hw) ||
+               mul_overflows(hw, channels, &chw) || image->len != chw;
+    if (bad)
+        return fail(VH_ERR_KERNEL, "invalid NCHW patchify shape image=" + std::to_string(image->len) +
+                                       ", channels=" + std::to_string(channels) +
+                                       ", height=" + std::to_string(height) +
+                                       ", width=" + std::to_string(width) +
+                                       ", patch=" + std::to_string(patch));
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    size_t len = (height / patch) * (width / patch) * channels * patch * patch;
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, len, &t, "patchify allocation"));
+    vh_status st = launch(s, "patchify_nchw", [&] {
+        return vh::launch_patchify(s.stream, image->ptr, t->ptr, height, width, patch, channels);
+    });
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_prepend_cls_add_pos_f32(const vh_runtime *rt, const vh_tensor *patches,
+                                                const vh_tensor *cls, const vh_tensor *position,
+                                                size_t patch_count, size_t embed,
+                                                vh_tensor **out) {
+    NEED(rt, "vh_prepend_cls_add_pos_f32");
+    NEED(patches, "vh_prepend_cls_add_pos_f32");
+    NEED(cls, "vh_prepend_cls_add_pos_f32");
+    NEED(position, "vh_prepend_cls_add_pos_f32");
+    NEED(out, "vh_prepend_cls_add_pos_f32");
+    size_t plen = 0, tlen = 0;
+    bool bad = embed == 0 || mul_overflows(patch_count, embed, &plen) ||
+               mul_overflows(patch_count + 1, embed, &tlen) || patches->len != plen ||
+               cls->len != embed || position->len != tlen;
+    if (bad)
+        return fail(VH_ERR_KERNEL, "invalid token assembly patches=" + std::to_string(patches->len) +
+                                       ", cls=" + std::to_string(cls->len) +
+                                       ", position=" + std::to_string(position->len) +
+                                       ", patch_count=" + std::to_string(patch_count) +
+                                       ", embed=" + std::to_string(embed));
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, tlen, &t, "token assembly allocation"));
+    vh_status st = launch(s, "prepend_cls_add_pos", [&] {
+        return vh::launch_prepend_cls_add_pos(s.stream, patches->ptr, cls->ptr, position->ptr,
+                                              t->ptr, patch_count, embed);
+    });
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+// =============================================================================
+// RoPE
+// =============================================================================
+
+extern "C" vh_status vh_rope2d_f32_in_place(const vh_runtime *rt, vh_tensor *x, size_t heads,
+                                            size_t n, size_t head_dim, const int64_t *pos_yx,
+                                            float frequency) {
+    NEED(rt, "vh_rope2d_f32_in_place");
+    NEED(x, "vh_rope2d_f32_in_place");
+    if (n && !pos_yx) return null_arg("vh_rope2d_f32_in_place positions");
+    size_t hn = 0, expected = 0;
+    if (mul_overflows(heads, n, &hn) || mul_overflows(hn, head_dim, &expected) || x->len != expected)
+        return mismatch(x->len, expected, "rope2d: x size mismatch");
+    if (head_dim % 4 != 0)
+        return fail(VH_ERR_KERNEL, "rope2d: head_dim must be divisible by 4, got " +
+                                       std::to_string(head_dim));
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    if (expected == 0) return VH_OK;
+    const float *rot = nullptr;
+    TRY(rope_table(s, pos_yx, n, head_dim, frequency, &rot));
+    return launch(s, "rope2d", [&] { return vh::launch_rope2d(s.stream, x->ptr, heads, n, head_dim, rot); });
+    GUARD_END
+}
+
+extern "C" vh_status vh_qk_norm_rope_f32_da3_base(const vh_runtime *rt, vh_tensor *q, vh_tensor *k,
+                                                  const vh_tensor *q_gamma,
+                                                  const vh_tensor *q_beta,
+                                                  const vh_tensor *k_gamma,
+                                                  const vh_tensor *k_beta,
+                                                  const vh_tensor *positions_yx, size_t heads,
+                                                  size_t tokens, float frequency, float epsilon) {
+    NEED(rt, "vh_qk_norm_rope_f32_da3_base");
+    NEED(q, "vh_qk_norm_rope_f32_da3_base");
+    NEED(k, "vh_qk_norm_rope_f32_da3_base");
+    NEED(q_gamma, "vh_qk_norm_rope_f32_da3_base");
+    NEED(q_beta, "vh_qk_norm_rope_f32_da3_base");
+    NEED(k_gamma, "vh_qk_norm_rope_f32_da3_base");
+    NEED(k_beta, "vh_qk_norm_rope_f32_da3_base");
+    NEED(positions_yx, "vh_qk_norm_rope_f32_da3_base");
+    size_t rows = 0, expected = 0;
+    bool bad = mul_overflows(heads, tokens, &rows) || mul_overflows(rows, 64, &expected) ||
+               q->len != expected || k->len != expected || q_gamma->len != 64 ||
+               q_beta->len != 64 || k_gamma->len != 64 || k_beta->len != 64 ||
+               positions_yx->len != tokens * 2;
+    if (bad) return mismatch(q->len, expected, "vh_qk_norm_rope_f32_da3_base");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    if (rows == 0) return VH_OK;
+    // The positions are a device tensor here (src/cuda.rs:1184), so the
+    // rotation table is built on the device from them.
+    float *rot = nullptr;
+    TRY(dalloc(s, tokens * 64, &rot, "RoPE table allocation"));
+    vh_status st = launch(s, "rope_table", [&] {
+        return vh::launch_rope_table_device(s.stream, positions_yx->ptr, tokens, frequency, rot);
+    });
+    if (!st)
+        st = launch(s, "qk_norm_rope", [&] {
+            return vh::launch_qk_norm_rope(s.stream, q->ptr, k->ptr, q_gamma->ptr, q_beta->ptr,
+                                           k_gamma->ptr, k_beta->ptr, rot, rows, tokens, epsilon);
+        });
+    hipFreeAsync(rot, s.stream);
+    return st;
+    GUARD_END
+}
+
+// =============================================================================
+// prepared projections
+// =============================================================================
+
+extern "C" vh_status vh_prepare_linear_f32(const vh_runtime *rt, size_t input_features,
+                                           size_t output_features, const float *weight,
+                                           const float *bias, const float *gamma,
+                                           vh_linear **out) {
+    NEED(rt, "vh_prepare_linear_f32");
+    NEED(out, "vh_prepare_linear_f32");
+    size_t kn = 0;
+    if (mul_overflows(input_features, output_features, &kn) || (kn && !weight) ||
+        (output_features && !bias))
+        return fail(VH_ERR_BLAS, "linear parameter shape K=" + std::to_string(input_features) +
+                                     ", N=" + std::to_string(output_features) +
+                                     " does not match the provided buffers");
+    if (input_features > INT32_MAX || output_features > INT32_MAX)
+        return fail(VH_ERR_BLAS, "linear dimension exceeds 2^31-1");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_linear *l = new vh_linear;
+    l->rt = rt->s;
+    vh_status st = prepare_lin(s, input_features, output_features, weight, bias, gamma, &l->L);
+    if (st) {
+        delete l;
+        return st;
+    }
+    *out = l;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" void vh_linear_free(vh_linear *linear) { delete linear; }
+extern "C" size_t vh_linear_input_features(const vh_linear *linear) { return linear ? linear->L.K : 0; }
+extern "C" size_t vh_linear_output_features(const vh_linear *linear) { return linear ? linear->L.N : 0; }
+
+static vh_status check_linear_input(const vh_linear *linear, const vh_tensor *input, size_t rows,
+                                    const char *name) {
+    NEED(linear, name);
+    NEED(input, name);
+    size_t expected = 0;
+    if (mul_overflows(rows, linear->L.K, &expected) || input->len != expected)
+        return fail(VH_ERR_BLAS, "linear input rows=" + std::to_string(rows) + ", K=" +
+                                     std::to_string(linear->L.K) +
+                                     " does not match device input length " +
+                                     std::to_string(input->len));
+    if (rows > INT32_MAX) return fail(VH_ERR_BLAS, "linear rows exceed 2^31-1");
+    return VH_OK;
+}
+
+extern "C" vh_status vh_linear_run(const vh_linear *linear, const vh_tensor *input, size_t rows,
+                                   vh_tensor **out) {
+    TRY(check_linear_input(linear, input, rows, "vh_linear_run"));
+    NEED(out, "vh_linear_run");
+    GUARD_BEGIN
+    RtState &s = *linear->rt;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(linear->rt, rows * linear->L.N, &t, "GEMM output allocation"));
+    vh_status st = run_lin(s, linear->L, input->ptr, rows, vh::Epi::Store, t->ptr, "gemm_bias_scale");
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_linear_run_chw(const vh_linear *linear, const vh_tensor *input,
+                                       size_t rows, vh_tensor **out) {
+    TRY(check_linear_input(linear, input, rows, "vh_linear_run_chw"));
+    NEED(out, "vh_linear_run_chw");
+    GUARD_BEGIN
+    RtState &s = *linear->rt;
+    TRY(set_device(s));
+    const size_t len = rows * linear->L.N;
+    if (rows == 0 || linear->L.N == 0)
+        return mismatch(len, len, "vh_linear_run_chw: token_to_chw needs tokens and channels");
+    float *tmp = nullptr;
+    TRY(dalloc(s, len, &tmp, "GEMM output allocation"));
+    vh_tensor *t = nullptr;
+    vh_status st = new_tensor(linear->rt, len, &t, "DPT CHW allocation");
+    if (!st) st = run_lin(s, linear->L, input->ptr, rows, vh::Epi::Store, tmp, "gemm_bias_scale");
+    if (!st)
+        st = launch(s, "token_to_chw", [&] {
+            return vh::launch_token_to_chw(s.stream, tmp, t->ptr, rows, linear->L.N);
+        });
+    hipFreeAsync(tmp, s.stream);
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_linear_run_gelu(const vh_linear *linear, const vh_tensor *input,
+                                        size_t rows, vh_tensor **out) {
+    TRY(check_linear_input(linear, input, rows, "vh_linear_run_gelu"));
+    NEED(out, "vh_linear_run_gelu");
+    if (linear->L.gamma)
+        return fail(VH_ERR_BLAS, "vh_linear_run_gelu: the linear carries a LayerScale gamma");
+    GUARD_BEGIN
+    RtState &s = *linear->rt;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(linear->rt, rows * linear->L.N, &t, "GEMM output allocation"));
+    vh_status st = run_lin(s, linear->L, input->ptr, rows, vh::Epi::Gelu, t->ptr, "gemm_bias_gelu");
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_linear_run_residual(const vh_linear *linear, const vh_tensor *input,
+                                            size_t rows, vh_tensor *residual) {
+    TRY(check_linear_input(linear, input, rows, "vh_linear_run_residual"));
+    NEED(residual, "vh_linear_run_residual");
+    if (residual->len != rows * linear->L.N)
+        return mismatch(residual->len, rows * linear->L.N, "vh_linear_run_residual");
+    RtState &s = *linear->rt;
+    TRY(set_device(s));
+    return run_lin(s, linear->L, input->ptr, rows, vh::Epi::Residual, residual->ptr,
+                   "gemm_bias_scale_residual");
+}
+
+extern "C" vh_status vh_linear_run_qkv_hnd(const vh_linear *linear, const vh_tensor *input,
+                                           size_t images, size_t tokens, size_t heads,
+                                           const int64_t *pos_yx, float frequency, vh_tensor **q,
+                                           vh_tensor **k, vh_tensor **v) {
+    NEED(linear, "vh_linear_run_qkv_hnd");
+    NEED(q, "vh_linear_run_qkv_hnd");
+    NEED(k, "vh_linear_run_qkv_hnd");
+    NEED(v, "vh_linear_run_qkv_hnd");
+    size_t rows = 0;
+    if (mul_overflows(images, tokens, &rows)) return mismatch(0, 0, "vh_linear_run_qkv_hnd");
+    TRY(check_linear_input(linear, input, rows, "vh_linear_run_qkv_hnd"));
+    if (heads == 0 || linear->L.N != heads * 3 * 64)
+        return fail(VH_ERR_BLAS, "vh_linear_run_qkv_hnd: output features " +
+                                     std::to_string(linear->L.N) + " != 3 * heads * 64");
+    if (linear->L.gamma)
+        return fail(VH_ERR_BLAS, "vh_linear_run_qkv_hnd: the QKV linear carries a gamma");
+    GUARD_BEGIN
+    RtState &s = *linear->rt;
+    TRY(set_device(s));
+    const float *rot = nullptr;
+    if (pos_yx && tokens) TRY(rope_table(s, pos_yx, tokens, 64, frequency, &rot));
+    const size_t len = rows * heads * 64;
+    vh_tensor *tq = nullptr, *tk = nullptr, *tv = nullptr;
+    vh_status st = new_tensor(linear->rt, len, &tq, "QKV output allocation");
+    if (!st) st = new_tensor(linear->rt, len, &tk, "QKV output allocation");
+    if (!st) st = new_tensor(linear->rt, len, &tv, "QKV output allocation");
+    if (!st) st = run_qkv(s, linear->L, input->ptr, images, tokens, heads, rot, tq->ptr, tk->ptr, tv->ptr);
+    if (st) {
+        delete tq;
+        delete tk;
+        delete tv;
+        return st;
+    }
+    *q = tq;
+    *k = tk;
+    *v = tv;
+    return VH_OK;
+    GUARD_END
+}
+
+// =============================================================================
+// Q8_0
+// =============================================================================
+
+namespace {
+#pragma pack(push, 1)
+struct BlockQ8 {
+    uint16_t d;
+    int8_t qs[32];
+};
+#pragma pack(pop)
+static_assert(sizeof(BlockQ8) == 34, "BlockQ8_0 is 34 bytes (src/lib.rs:33-38)");
+
+vh_status new_q8(const Rt &rt, size_t rows, size_t k, vh_q8_tensor **out) {
+    vh_q8_tensor *t = new vh_q8_tensor;
+    t->rt = rt;
+    t->rows = rows;
+    t->k = k;
+    vh_status st = dalloc(*rt, rows * k, &t->qs, "Q8_0 allocation");
+    if (!st) st = dalloc(*rt, rows * (k / 32), &t->d, "Q8_0 allocation");
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+}
+}  // namespace
+
+extern "C" vh_status vh_q8_0_upload(const vh_runtime *rt, const void *blocks, size_t rows,
+                                    size_t k, vh_q8_tensor **out) {
+    NEED(rt, "vh_q8_0_upload");
+    NEED(out, "vh_q8_0_upload");
+    size_t n = 0;
+    if (k % 32 != 0 || mul_overflows(rows, k, &n))
+        return fail(VH_ERR_KERNEL, "vh_q8_0_upload: k must be a multiple of 32, got " + std::to_string(k));
+    if (n && !blocks) return null_arg("vh_q8_0_upload blocks");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    const size_t nb = n / 32;
+    std::vector<int8_t> qs(n);
+    std::vector<uint16_t> d(nb);
+    const BlockQ8 *src = static_cast<const BlockQ8 *>(blocks);
+    for (size_t b = 0; b < nb; b++) {
+        BlockQ8 blk;
+        std::memcpy(&blk, src + b, sizeof(blk));
+        d[b] = blk.d;
+        std::memcpy(&qs[b * 32], blk.qs, 32);
+    }
+    vh_q8_tensor *t = nullptr;
+    TRY(new_q8(rt->s, rows, k, &t));
+    vh_status st = h2d(s, t->qs, qs.data(), n, "Q8_0 upload");
+    if (!st) st = h2d(s, t->d, d.data(), nb * 2, "Q8_0 upload");
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_q8_0_download(const vh_runtime *rt, const vh_q8_tensor *tensor,
+                                      void *blocks, size_t nblocks) {
+    NEED(rt, "vh_q8_0_download");
+    NEED(tensor, "vh_q8_0_download");
+    const size_t nb = tensor->rows * tensor->k / 32;
+    if (nblocks != nb) return mismatch(nblocks, nb, "vh_q8_0_download");
+    if (nb && !blocks) return null_arg("vh_q8_0_download blocks");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    std::vector<int8_t> qs(nb * 32);
+    std::vector<uint16_t> d(nb);
+    hipError_t e = hipSuccess;
+    if (nb) {
+        e = hipMemcpyAsync(qs.data(), tensor->qs, nb * 32, hipMemcpyDeviceToHost, s.stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(d.data(), tensor->d, nb * 2, hipMemcpyDeviceToHost, s.stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(s.stream);
+    }
+    if (e != hipSuccess) return fail(VH_ERR_DOWNLOAD, hip_msg("Q8_0 download", e));
+    BlockQ8 *dst = static_cast<BlockQ8 *>(blocks);
+    for (size_t b = 0; b < nb; b++) {
+        BlockQ8 blk;
+        blk.d = d[b];
+        std::memcpy(blk.qs, &qs[b * 32], 32);
+        std::memcpy(dst + b, &blk, sizeof(blk));
+    }
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" void vh_q8_tensor_free(vh_q8_tensor *tensor) { delete tensor; }
+extern "C" size_t vh_q8_tensor_rows(const vh_q8_tensor *t) { return t ? t->rows : 0; }
+extern "C" size_t vh_q8_tensor_k(const vh_q8_tensor *t) { return t ? t->k : 0; }
+
+extern "C" vh_status vh_quantize_q8_0(const vh_runtime *rt, const vh_tensor *x, size_t rows,
+                                      size_t k, vh_q8_tensor **out) {
+    NEED(rt, "vh_quantize_q8_0");
+    NEED(x, "vh_quantize_q8_0");
+    NEED(out, "vh_quantize_q8_0");
+    size_t n = 0;
+    if (mul_overflows(rows, k, &n) || x->len != n)
+        return mismatch(x->len, n, "x.len() must be out.len()*QK8_0");
+    if (k % 32 != 0)
+        return fail(VH_ERR_KERNEL, "vh_quantize_q8_0: k must be a multiple of 32, got " + std::to_string(k));
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_q8_tensor *t = nullptr;
+    TRY(new_q8(rt->s, rows, k, &t));
+    vh_status st = launch(s, "quantize_q8_0", [&] {
+        return vh::launch_quantize_q8_0(s.stream, x->ptr, t->qs, t->d, rows, k);
+    });
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_gemm_q8_0(const vh_runtime *rt, const vh_q8_tensor *a_q,
+                                  const vh_q8_tensor *b_q, size_t m, size_t n, size_t k,
+                                  vh_tensor **out) {
+    NEED(rt, "vh_gemm_q8_0");
+    NEED(a_q, "vh_gemm_q8_0");
+    NEED(b_q, "vh_gemm_q8_0");
+    NEED(out, "vh_gemm_q8_0");
+    if (k % 32 != 0)
+        return fail(VH_ERR_KERNEL, "k must be a multiple of QK8_0, got " + std::to_string(k));
+    if (a_q->rows != m || a_q->k != k || b_q->rows != n || b_q->k != k)
+        return mismatch(a_q->rows * a_q->k, m * k, "vh_gemm_q8_0 operand shape");
+    if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
+        return fail(VH_ERR_KERNEL, "vh_gemm_q8_0 dimension exceeds 2^31-1");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, m * n, &t, "Q8_0 GEMM output allocation"));
+    vh_status st = launch(s, "gemm_q8_0", [&] {
+        return vh::launch_gemm_q8_0(s.stream, a_q->qs, a_q->d, b_q->qs, b_q->d, t->ptr, m, n, k);
+    });
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+// =============================================================================
+// DA3-BASE encoder block
+// =============================================================================
+
+namespace {
+constexpr size_t kDim = 768, kHeads = 12, kMlp = 3072;
+
+vh_status upload_small(RtState &s, const float *h, size_t n, float **out, const char *what) {
+    if (!h) return null_arg(what);
+    return upload_array(s, h, n, out, what);
+}
+
+vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size_t tokens,
+                    const int64_t *pos, float freq, float eps) {
+    const size_t M = images * tokens;
+    const size_t D = kDim;
+    float *ws = nullptr;
+    TRY(workspace(s, M * (5 * D + kMlp), &ws));
+    float *h = ws, *q = h + M * D, *k = q + M * D, *v = k + M * D, *att = v + M * D,
+          *f = att + M * D;
+    const float *rot = nullptr;
+    if (pos) TRY(rope_table(s, pos, tokens, 64, freq, &rot));
+    TRY(launch(s, "layernorm", [&] {
+        return vh::launch_layernorm(s.stream, x, b.ln1_g, b.ln1_b, h, M, D, eps);
+    }));
+    TRY(run_qkv(s, b.qkv, h, images, tokens, kHeads, rot, q, k, v));
+    TRY(launch(s, "flash_attention", [&] {
+        return vh::launch_flash_attention(s.stream, q, k, v, att, images * kHeads, tokens, kHeads, true);
+    }));
+    TRY(run_lin(s, b.proj, att, M, vh::Epi::Residual, x, "gemm_proj_residual"));
+    TRY(launch(s, "layernorm", [&] {
+        return vh::launch_layernorm(s.stream, x, b.ln2_g, b.ln2_b, h, M, D, eps);
+    }));
+    TRY(run_lin(s, b.fc1, h, M, vh::Epi::Gelu, f, "gemm_fc1_gelu"));
+    TRY(run_lin(s, b.fc2, f, M, vh::Epi::Residual, x, "gemm_fc2_residual"));
+    return VH_OK;
+}
+
+vh_status check_block_x(const vh_tensor *x, size_t images, size_t tokens) {
+    size_t m = 0, len = 0;
+    if (mul_overflows(images, tokens, &m) || mul_overflows(m, kDim, &len) || x->len != len)
+        return mismatch(x->len, len, "DA3 block input");
+    if (m > INT32_MAX / 4 || images * kHeads > 65535)
+        return fail(VH_ERR_KERNEL, "DA3 block shape exceeds the launch grid");
+    return VH_OK;
+}
+}  // namespace
+
+extern "C" vh_status vh_block_prepare(const vh_runtime *rt, const vh_block_params *p,
+                                      vh_block **out) {
+    NEED(rt, "vh_block_prepare");
+    NEED(p, "vh_block_prepare");
+    NEED(out, "vh_block_prepare");
+    const float *req[] = {p->ln1_gamma, p->ln1_beta, p->w_qkv, p->b_qkv, p->w_proj,
+                          p->b_proj,    p->ls1,      p->ln2_gamma, p->ln2_beta, p->w_fc1,
+                          p->b_fc1,     p->w_fc2,    p->b_fc2, p->ls2};
+    for (const float *r : req)
+        if (!r) return null_arg("vh_block_prepare parameter");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_block *b = new vh_block;
+    b->rt = rt->s;
+    vh_status st = prepare_lin(s, kDim, 3 * kDim, p->w_qkv, p->b_qkv, nullptr, &b->qkv);
+    if (!st) st = prepare_lin(s, kDim, kDim, p->w_proj, p->b_proj, p->ls1, &b->proj);
+    if (!st) st = prepare_lin(s, kDim, kMlp, p->w_fc1, p->b_fc1, nullptr, &b->fc1);
+    if (!st) st = prepare_lin(s, kMlp, kDim, p->w_fc2, p->b_fc2, p->ls2, &b->fc2);
+    if (!st) st = upload_small(s, p->ln1_gamma, kDim, &b->ln1_g, "ln1 gamma");
+    if (!st) st = upload_small(s, p->ln1_beta, kDim, &b->ln1_b, "ln1 beta");
+    if (!st) st = upload_small(s, p->ln2_gamma, kDim, &b->ln2_g, "ln2 gamma");
+    if (!st) st = upload_small(s, p->ln2_beta, kDim, &b->ln2_b, "ln2 beta");
+    if (st) {
+        delete b;
+        return st;
+    }
+    *out = b;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" void vh_block_free(vh_block *block) { delete block; }
+
+extern "C" vh_status vh_vit_block_run(const vh_runtime *rt, const vh_block *block, vh_tensor *x,
+                                      size_t images, size_t tokens, const int64_t *pos_yx,
+                                      float rope_frequency, float epsilon) {
+    NEED(rt, "vh_vit_block_run");
+    NEED(block, "vh_vit_block_run");
+    NEED(x, "vh_vit_block_run");
+    TRY(check_block_x(x, images, tokens));
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    if (images * tokens == 0) return VH_OK;
+    return block_run(s, *block, x->ptr, images, tokens, pos_yx, rope_frequency, epsilon);
+    GUARD_END
+}
+
+extern "C" vh_status vh_encoder_run(const vh_runtime *rt, const vh_block *const *blocks,
+                                    size_t layers, vh_tensor *x, size_t images, size_t tokens,
+                                    const int64_t *pos_yx, float rope_frequency, float epsilon) {
+    NEED(rt, "vh_encoder_run");
+    NEED(x, "vh_encoder_run");
+    if (layers && !blocks) return null_arg("vh_encoder_run blocks");
+    for (size_t i = 0; i < layers; i++)
+        if (!blocks[i]) return null_arg("vh_encoder_run block");
+    TRY(check_block_x(x, images, tokens));
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    if (images * tokens == 0) return VH_OK;
+    for (size_t i = 0; i < layers; i++)
+        TRY(block_run(s, *blocks[i], x->ptr, images, tokens, pos_yx, rope_frequency, epsilon));
+    return VH_OK;
+    GUARD_END
+}
+
+// =============================================================================
+// profiling
+// =============================================================================
+
+extern "C" vh_status vh_profile_enable(vh_runtime *rt, int enabled) {
+    NEED(rt, "vh_profile_enable");
+    rt->s->profile = enabled != 0;
+    return VH_OK;
+}
+
+extern "C" vh_status vh_profile_reset(vh_runtime *rt) {
+    NEED(rt, "vh_profile_reset");
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    hipStreamSynchronize(s.stream);
+    for (auto &p : s.pending) {
+        hipEventDestroy(p.a);
+        hipEventDestroy(p.b);
+    }
+    s.pending.clear();
+    s.totals.clear();
+    return VH_OK;
+}
+
+extern "C" vh_status vh_profile_report(vh_runtime *rt, char *buf, size_t buflen) {
+    NEED(rt, "vh_profile_report");
+    if (buflen && !buf) return null_arg("vh_profile_report buf");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    hipError_t e = hipStreamSynchronize(s.stream);
+    if (e != hipSuccess) return fail(VH_ERR_KERNEL, hip_msg("profile synchronize", e));
+    for (auto &p : s.pending) {
+        float ms = 0.0f;
+        hipEventElapsedTime(&ms, p.a, p.b);
+        auto &t = s.totals[p.name];
+        t.first += 1;
+        t.second += ms;
+        hipEventDestroy(p.a);
+        hipEventDestroy(p.b);
+    }
+    s.pending.clear();
+    std::string out;
+    char line[256];
+    for (auto &kv : s.totals) {
+        std::snprintf(line, sizeof(line), "%s %llu %.6f\n", kv.first.c_str(), kv.second.first,
+                      kv.second.second);
+        out += line;
+    }
+    if (buflen) {
+        size_t n = out.size() < buflen - 1 ? out.size() : buflen - 1;
+        std::memcpy(buf, out.data(), n);
+        buf[n] = '\0';
+    }
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_timer_start(vh_runtime *rt) {
+    NEED(rt, "vh_timer_start");
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    if (!s.t0 && hipEventCreate(&s.t0) != hipSuccess) return fail(VH_ERR_KERNEL, "event create");
+    if (!s.t1 && hipEventCreate(&s.t1) != hipSuccess) return fail(VH_ERR_KERNEL, "event create");
+    hipError_t e = hipEventRecord(s.t0, s.stream);
+    if (e != hipSuccess) return fail(VH_ERR_KERNEL, hip_msg("event record", e));
+    return VH_OK;
+}
+
+extern "C" vh_status vh_timer_stop(vh_runtime *rt, float *elapsed_ms) {
+    NEED(rt, "vh_timer_stop");
+    NEED(elapsed_ms, "vh_timer_stop");
+    RtState &s = *rt->s;
+    if (!s.t0) return fail(VH_ERR_KERNEL, "vh_timer_stop without vh_timer_start");
+    TRY(set_device(s));
+    hipError_t e = hipEventRecord(s.t1, s.stream);
+    if (e == hipSuccess) e = hipEventSynchronize(s.t1);
+    if (e == hipSuccess) e = hipEventElapsedTime(elapsed_ms, s.t0, s.t1);
+    if (e != hipSuccess) return fail(VH_ERR_KERNEL, hip_msg("timer", e));
+    return VH_OK;
+}
