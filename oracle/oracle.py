@@ -61,6 +61,7 @@ def _declare(L):
     sig("vko_add_bias_rows", None, _f32p, _sz, _sz, _f32p)
     sig("vko_layernorm", None, _f32p, _sz, _sz, _f32p, _f32p, ctypes.c_float)
     sig("vko_erf", ctypes.c_float, ctypes.c_float)
+    sig("vko_cephes_exp", ctypes.c_float, ctypes.c_float)
     sig("vko_gelu", None, _f32p, _sz)
     sig("vko_gelu_avx512", None, _f32p, _sz)
     sig("vko_gelu_avx512_lanes", None, _f32p, _sz)
@@ -170,6 +171,11 @@ def layernorm(x, rows, cols, gamma, beta, eps):
 
 def erf(x: float) -> float:
     return float(lib().vko_erf(ctypes.c_float(x)))
+
+
+def cephes_exp(x: float) -> float:
+    """The AVX-512 Cephes exp (src/simd_avx512.rs:22-69), one lane."""
+    return float(lib().vko_cephes_exp(ctypes.c_float(x)))
 
 
 def gelu(x):

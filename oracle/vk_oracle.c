@@ -392,6 +392,8 @@ static inline float cephes_exp_scalar(float x) {
     return y * p2;
 }
 
+float vko_cephes_exp(float x) { return cephes_exp_scalar(x); }
+
 __attribute__((target("avx512f,fma"))) static inline __m512 exp_avx512(__m512 x) {
     const __m512 one = _mm512_set1_ps(1.0f);
     x = _mm512_min_ps(x, _mm512_set1_ps(CEPHES_HI));

@@ -64,6 +64,9 @@ void vko_gemm_q8_0_avx512(size_t m, size_t n, size_t k, const vko_block_q8_0 *a_
 void vko_kernels_gemm_q8_0(size_t m, size_t n, size_t k, const vko_block_q8_0 *a_q,
                            const vko_block_q8_0 *b_q, float *c);
 
+/* Cephes exp of src/simd_avx512.rs:22-69, one lane in scalar code. */
+float vko_cephes_exp(float x);
+
 /* ---- AVX-512 elementwise (src/simd_avx512.rs) + Kernels dispatch -------- */
 void vko_gelu_avx512(float *x, size_t n);
 void vko_gelu_avx512_lanes(float *x, size_t n); /* same arithmetic in scalar code */
