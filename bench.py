@@ -128,6 +128,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run 5 residual-add kernels over 16M floats (reads 128 MiB, "
+                         "writes 64 MiB each) to scale PMC byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -136,6 +139,16 @@ def main() -> int:
         return 2
 
     gpu = gpu_block(args.steps, args.warmup)
+    if args.calibrate:
+        import vestra_hip as vh
+
+        rt = vh.Runtime(0)
+        n = 16 * 1024 * 1024
+        a, b = rt.upload_f32(np.ones(n, np.float32)), rt.upload_f32(np.ones(n, np.float32))
+        for _ in range(5):
+            rt.add_f32_in_place(a, b)
+        rt.synchronize()
+        log("calibration: 5 x add_kernel over 16M floats (128 MiB read, 64 MiB written)")
     ker = gpu["kernels"]
     gemm_attn = [n for n in FLOPS if n in ker]
     t_us = sum(ker[n]["avg_us"] * ker[n]["launches_per_block"] for n in gemm_attn)

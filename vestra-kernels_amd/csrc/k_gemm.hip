@@ -2,26 +2,31 @@
 //
 // C[m,n] = sum_k A[m,k] * Bt[n,k]; A is the activation (row-major), Bt the
 // weight prepared once in [out, in] order so both operands stream k-contiguous
-// rows.  A 256-thread workgroup (4 wave64s) owns a BM x BN tile; BK = 32
-// slices of A and Bt are double-buffered in LDS with rows padded to 36 floats
-// (16-byte fragment reads of 16 consecutive rows then touch 64 distinct
-// banks).  Each wave computes a (BM/WM) x (BN/WN) sub-tile with
-// v_mfma_f32_16x16x4_f32: one ds_read_b128 per 16-row fragment feeds four
-// MFMA k-steps (lane group h supplies k = kk+4h+s at step s).
+// rows.  A workgroup of WM x WN wave64s owns a BM x BN tile; BK-wide slices of
+// A and Bt are double-buffered in LDS with rows padded by 4 floats (16-byte
+// fragment reads of 16 consecutive rows then touch 64 distinct banks).  Each
+// wave computes a (BM/WM) x (BN/WN) sub-tile with v_mfma_f32_16x16x4_f32: one
+// ds_read_b128 per 16-row fragment feeds four MFMA k-steps (lane group h
+// supplies k = kk+4h+s at step s).
+//
+// Split-K (grid.z > 1) is deterministic: each split writes its partial tile
+// to a workspace and a reduction kernel sums the partials in split order
+// before applying the epilogue.
 //
 // Epilogues (all separately rounded, as the reference's):
 //   Store    : c = (acc + bias) * gamma          (CudaLinearF32::run)
 //   Gelu     : c = gelu(acc + bias)              (fc1, Kernels::gelu forms)
 //   Residual : c = c + (acc + bias) * gamma      (out-proj / fc2 + residual)
 //   Qkv      : head-major Q/K/V with bias and the 2-D RoPE rotation of Q, K
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+
 #include "common.h"
 #include "kernels.h"
 
 namespace vh {
 namespace {
-
-constexpr int BK = 32;
-constexpr int LDK = BK + 4;
 
 struct EpiArgs {
     float *c;
@@ -31,70 +36,97 @@ struct EpiArgs {
     int tokens, heads;
     const float *rot;
     size_t tail_start;
+    float *partial;  // split-K: raw partial tiles [split][M][N]
 };
 
-template <int BM, int BN, int WM, int WN, Epi EPI>
-__global__ __launch_bounds__(256) void gemm_nt_kernel(const float *__restrict__ A,
-                                                      const float *__restrict__ Bt, int M, int N,
-                                                      int K, EpiArgs ep) {
+// Applies a Store / Gelu / Residual epilogue to one output element.
+template <Epi EPI>
+__device__ __forceinline__ void epilogue_store(const EpiArgs &ep, size_t idx, int col, float v) {
+    if (ep.bias) v = add_rn(v, ep.bias[col]);
+    if constexpr (EPI == Epi::Store) {
+        if (ep.gamma) v = mul_rn(v, ep.gamma[col]);
+        ep.c[idx] = v;
+    } else if constexpr (EPI == Epi::Gelu) {
+        ep.c[idx] = idx < ep.tail_start ? gelu_avx512_form(v) : gelu_scalar_form(v);
+    } else {
+        if (ep.gamma) v = mul_rn(v, ep.gamma[col]);
+        ep.c[idx] = add_rn(ep.c[idx], v);
+    }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT>
+__global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__restrict__ A,
+                                                              const float *__restrict__ Bt,
+                                                              int M, int N, int K,
+                                                              int k_per_split, EpiArgs ep) {
+    constexpr int NT = WM * WN * 64;
+    constexpr int LDK = BK + 4;
+    constexpr int CPR = BK / 4;  // float4 chunks per row slice
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 16, FN = TN / 16;
-    constexpr int ACH = BM * BK / 4 / 256;
-    constexpr int BCH = BN * BK / 4 / 256;
-    static_assert(WM * WN == 4, "four waves");
-    static_assert(ACH >= 1 && BCH >= 1, "tile too small for 256 threads");
-    static_assert(EPI != Epi::Qkv || TN == 64, "QKV epilogue needs one head per wave tile");
+    constexpr int ACH = BM * CPR / NT;
+    constexpr int BCH = BN * CPR / NT;
+    static_assert((BM * CPR) % NT == 0 && (BN * CPR) % NT == 0, "tile / thread mismatch");
+    static_assert(ACH >= 1 && BCH >= 1, "tile too small for the thread count");
+    static_assert(TM % 16 == 0 && TN % 16 == 0 && BK % 16 == 0, "fragment shape");
+    static_assert(EPI != Epi::Qkv || TN == 32 || TN == 64,
+                  "QKV epilogue needs whole 32-wide RoPE halves of one head per wave tile");
 
-    __shared__ __attribute__((aligned(16))) float As[2][BM * LDK];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BN * LDK];
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float *As = smem;                    // [2][BM * LDK]
+    float *Bs = smem + 2 * BM * LDK;     // [2][BN * LDK]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lh = lane >> 4;
     const int wm = wave / WN, wn = wave % WN;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kbeg = blockIdx.z * k_per_split;
+    const int kend = min(K, kbeg + k_per_split);
     const bool vec = (K & 3) == 0;
 
     f32x4 ra[ACH], rb[BCH];
     auto gload = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
-            int c = tid + i * 256, row = c >> 3, kq = (c & 7) * 4;
+            int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
             int gm = m0 + row, gk = k0 + kq;
             const float *p = A + (size_t)gm * K + gk;
-            if (vec && gm < M && gk < K) {
+            if (vec && gm < M && gk < kend) {
                 ra[i] = *reinterpret_cast<const f32x4 *>(p);
             } else {
                 f32x4 t;
 #pragma unroll
-                for (int e = 0; e < 4; e++) t[e] = (gm < M && gk + e < K) ? p[e] : 0.0f;
+                for (int e = 0; e < 4; e++) t[e] = (gm < M && gk + e < kend) ? p[e] : 0.0f;
                 ra[i] = t;
             }
         }
 #pragma unroll
         for (int i = 0; i < BCH; i++) {
-            int c = tid + i * 256, row = c >> 3, kq = (c & 7) * 4;
+            int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
             int gn = n0 + row, gk = k0 + kq;
             const float *p = Bt + (size_t)gn * K + gk;
-            if (vec && gn < N && gk < K) {
+            if (vec && gn < N && gk < kend) {
                 rb[i] = *reinterpret_cast<const f32x4 *>(p);
             } else {
                 f32x4 t;
 #pragma unroll
-                for (int e = 0; e < 4; e++) t[e] = (gn < N && gk + e < K) ? p[e] : 0.0f;
+                for (int e = 0; e < 4; e++) t[e] = (gn < N && gk + e < kend) ? p[e] : 0.0f;
                 rb[i] = t;
             }
         }
     };
     auto lstore = [&](int buf) {
+        float *as = As + buf * BM * LDK;
+        float *bs = Bs + buf * BN * LDK;
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
-            int c = tid + i * 256, row = c >> 3, kq = (c & 7) * 4;
-            *reinterpret_cast<f32x4 *>(&As[buf][row * LDK + kq]) = ra[i];
+            int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
+            *reinterpret_cast<f32x4 *>(&as[row * LDK + kq]) = ra[i];
         }
 #pragma unroll
         for (int i = 0; i < BCH; i++) {
-            int c = tid + i * 256, row = c >> 3, kq = (c & 7) * 4;
-            *reinterpret_cast<f32x4 *>(&Bs[buf][row * LDK + kq]) = rb[i];
+            int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
+            *reinterpret_cast<f32x4 *>(&bs[row * LDK + kq]) = rb[i];
         }
     };
 
@@ -105,8 +137,8 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const float *__restrict__ 
         for (int j = 0; j < FN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     auto compute = [&](int buf) {
-        const float *as = As[buf];
-        const float *bs = Bs[buf];
+        const float *as = As + buf * BM * LDK;
+        const float *bs = Bs + buf * BN * LDK;
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 16) {
             f32x4 a[FM], b[FN];
@@ -127,14 +159,14 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const float *__restrict__ 
         }
     };
 
-    const int ktiles = (K + BK - 1) / BK;
-    gload(0);
+    const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    gload(kbeg);
     lstore(0);
     __syncthreads();
     for (int t = 0; t < ktiles; t++) {
         const int cur = t & 1;
         const bool next = t + 1 < ktiles;
-        if (next) gload((t + 1) * BK);
+        if (next) gload(kbeg + (t + 1) * BK);
         compute(cur);
         if (next) lstore(cur ^ 1);
         __syncthreads();
@@ -142,11 +174,27 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const float *__restrict__ 
 
     // C fragment layout: register r of lane l holds row 4*(l/16)+r, column l%16.
     const int rbase = m0 + wm * TM + 4 * lh;
-    if constexpr (EPI == Epi::Qkv) {
-        const int colw = n0 + wn * TN;  // first column of this wave's head
+    if constexpr (SPLIT) {
+        float *part = ep.partial + (size_t)blockIdx.z * M * N;
+        const int cbase = n0 + wn * TN + li;
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int col = cbase + j * 16;
+            if (col >= N) continue;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = rbase + i * 16 + r;
+                    if (row < M) part[(size_t)row * N + col] = acc[i][j][r];
+                }
+        }
+    } else if constexpr (EPI == Epi::Qkv) {
+        const int colw = n0 + wn * TN;  // first column of this wave's sub-tile
         if (colw >= N) return;
         const int per = ep.heads * 64;
         const int group = colw / per, head = (colw % per) / 64;
+        const int d0 = colw % 64;       // 0 or 32 (32-wide tile) / 0 (64-wide)
         float *dst = group == 0 ? ep.q : (group == 1 ? ep.k : ep.v);
         const bool rope = ep.rot != nullptr && group < 2;
         float bias[FN];
@@ -164,17 +212,18 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const float *__restrict__ 
                 for (int j = 0; j < FN; j++) vals[j] = add_rn(acc[i][j][r], bias[j]);
                 if (rope) {
                     // rope::rotate_half (src/rope.rs:84-93): dims (i, i+16) of
-                    // each 32-wide axis half sit in fragments (2a, 2a+1).
+                    // each 32-wide axis half sit in fragments (2h, 2h+1).
 #pragma unroll
-                    for (int axis = 0; axis < 2; axis++) {
+                    for (int h = 0; h < FN / 2; h++) {
+                        const int axis = d0 / 32 + h;
                         const float *rr = ep.rot + (((size_t)t * 2 + axis) * 16 + li) * 2;
                         const float sn = rr[0], cs = rr[1];
-                        const float a = vals[2 * axis], b = vals[2 * axis + 1];
-                        vals[2 * axis] = sub_rn(mul_rn(a, cs), mul_rn(b, sn));
-                        vals[2 * axis + 1] = add_rn(mul_rn(b, cs), mul_rn(a, sn));
+                        const float a = vals[2 * h], b = vals[2 * h + 1];
+                        vals[2 * h] = sub_rn(mul_rn(a, cs), mul_rn(b, sn));
+                        vals[2 * h + 1] = add_rn(mul_rn(b, cs), mul_rn(a, sn));
                     }
                 }
-                float *orow = dst + (((size_t)img * ep.heads + head) * ep.tokens + t) * 64;
+                float *orow = dst + (((size_t)img * ep.heads + head) * ep.tokens + t) * 64 + d0;
 #pragma unroll
                 for (int j = 0; j < FN; j++) orow[j * 16 + li] = vals[j];
             }
@@ -184,43 +233,137 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const float *__restrict__ 
         for (int j = 0; j < FN; j++) {
             const int col = cbase + j * 16;
             if (col >= N) continue;
-            const float b = ep.bias ? ep.bias[col] : 0.0f;
-            const float g = ep.gamma ? ep.gamma[col] : 1.0f;
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int row = rbase + i * 16 + r;
-                    if (row >= M) continue;
-                    const size_t idx = (size_t)row * N + col;
-                    float v = acc[i][j][r];
-                    if (ep.bias) v = add_rn(v, b);
-                    if constexpr (EPI == Epi::Store) {
-                        if (ep.gamma) v = mul_rn(v, g);
-                        ep.c[idx] = v;
-                    } else if constexpr (EPI == Epi::Gelu) {
-                        ep.c[idx] = idx < ep.tail_start ? gelu_avx512_form(v) : gelu_scalar_form(v);
-                    } else {
-                        if (ep.gamma) v = mul_rn(v, g);
-                        ep.c[idx] = add_rn(ep.c[idx], v);
-                    }
+                    if (row < M) epilogue_store<EPI>(ep, (size_t)row * N + col, col, acc[i][j][r]);
                 }
         }
     }
 }
 
-template <int BM, int BN, int WM, int WN, Epi EPI>
-hipError_t run(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
-    dim3 grid((unsigned)((g.n + BN - 1) / BN), (unsigned)((g.m + BM - 1) / BM));
-    gemm_nt_kernel<BM, BN, WM, WN, EPI>
-        <<<grid, 256, 0, s>>>(g.a, g.bt, (int)g.m, (int)g.n, (int)g.k, ep);
+// Sums the split-K partials in split order, then applies the epilogue.
+template <Epi EPI>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(int splits, int M, int N, EpiArgs ep) {
+    const size_t mn = (size_t)M * N;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < mn; idx += stride) {
+        float v = ep.partial[idx];
+        for (int s = 1; s < splits; s++) v = add_rn(v, ep.partial[(size_t)s * mn + idx]);
+        epilogue_store<EPI>(ep, idx, (int)(idx % N), v);
+    }
+}
+
+struct Tile {
+    int bm, bn, bk, wm, wn;
+};
+
+template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT>
+hipError_t run_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int splits) {
+    constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 4) * sizeof(float);
+    auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, SPLIT>;
+    static bool configured = false;
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    const int kps = (int)(((g.k + splits - 1) / splits + BK - 1) / BK * BK);
+    dim3 grid((unsigned)((g.n + BN - 1) / BN), (unsigned)((g.m + BM - 1) / BM), (unsigned)splits);
+    kernel<<<grid, WM * WN * 64, lds, s>>>(g.a, g.bt, (int)g.m, (int)g.n, (int)g.k, kps, ep);
     return hipGetLastError();
 }
 
+template <Epi EPI, bool SPLIT>
+hipError_t run_cfg(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, const Tile &t, int splits) {
+#define VH_TILE(BM, BN, BK, WM, WN)                                                    \
+    if constexpr (EPI != Epi::Qkv || (BN) / (WN) == 64 || (BN) / (WN) == 32) {           \
+        if (t.bm == BM && t.bn == BN && t.bk == BK && t.wm == WM && t.wn == WN)        \
+            return run_tile<BM, BN, BK, WM, WN, EPI, SPLIT>(s, g, ep, splits);          \
+    }
+    VH_TILE(64, 128, 32, 2, 2)
+    VH_TILE(64, 64, 32, 2, 2)
+    VH_TILE(128, 128, 32, 2, 2)
+    VH_TILE(64, 128, 32, 2, 4)
+    VH_TILE(32, 128, 32, 1, 4)
+    VH_TILE(32, 64, 32, 2, 2)
+    VH_TILE(64, 128, 64, 2, 2)
+    VH_TILE(128, 64, 32, 2, 2)
+    VH_TILE(64, 64, 64, 2, 2)
+    VH_TILE(128, 128, 32, 2, 4)
+#undef VH_TILE
+    return hipErrorInvalidValue;
+}
+
+// VESTRA_HIP_GEMM_TILE="BMxBNxBKxWMxWNxSPLIT" overrides the per-shape choice
+// (A/B studies); unknown tiles fall back to the default.
+bool tile_override(Tile *t, int *splits) {
+    const char *e = std::getenv("VESTRA_HIP_GEMM_TILE");
+    if (!e || !*e) return false;
+    Tile o{};
+    int sp = 1;
+    if (std::sscanf(e, "%dx%dx%dx%dx%dx%d", &o.bm, &o.bn, &o.bk, &o.wm, &o.wn, &sp) < 5) return false;
+    *t = o;
+    *splits = sp > 0 ? sp : 1;
+    return true;
+}
+
+// Per-shape defaults from the tile sweep on MI355X (DA3 projections at 865
+// and 4 x 865 tokens): eight-wave workgroups, split-K 3 for the N = 768
+// projections so that the grid covers the 256 CUs.
+void default_tile(const GemmArgs &g, Tile *t, int *splits) {
+    *splits = 1;
+    const bool narrow = g.n <= 1024;
+    if (g.m <= 1024) {
+        if (narrow) {
+            *t = Tile{64, 128, 32, 2, 4};
+            *splits = g.k >= 384 ? 3 : 1;
+        } else if (g.epi == Epi::Qkv || g.n < 3072) {
+            *t = Tile{64, 128, 32, 2, 4};
+        } else {
+            *t = Tile{32, 128, 32, 1, 4};
+        }
+    } else {
+        if (narrow) {
+            *t = Tile{128, 128, 32, 2, 4};
+            *splits = g.k >= 384 ? 3 : 1;
+        } else if (g.epi == Epi::Qkv || g.n < 3072) {
+            *t = Tile{128, 128, 32, 2, 4};
+        } else {
+            *t = Tile{64, 128, 32, 2, 4};
+        }
+    }
+}
+
 template <Epi EPI>
-hipError_t dispatch(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
-    if (g.n >= 2048) return run<64, 128, 2, 2, EPI>(s, g, ep);
-    return run<64, 64, 2, 2, EPI>(s, g, ep);
+hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
+    Tile t;
+    int splits;
+    if (!tile_override(&t, &splits)) default_tile(g, &t, &splits);
+    if (EPI == Epi::Qkv) splits = 1;
+    if (splits > 1 && (g.ws == nullptr || g.ws_floats < (size_t)splits * g.m * g.n)) splits = 1;
+    if (splits == 1) {
+        hipError_t e = run_cfg<EPI, false>(s, g, ep, t, 1);
+        if (e == hipErrorInvalidValue) {
+            default_tile(g, &t, &splits);
+            e = run_cfg<EPI, false>(s, g, ep, t, 1);
+        }
+        return e;
+    }
+    if constexpr (EPI == Epi::Qkv) {
+        return hipErrorInvalidValue;
+    } else {
+        ep.partial = g.ws;
+        hipError_t e = run_cfg<EPI, true>(s, g, ep, t, splits);
+        if (e != hipSuccess) return e;
+        size_t mn = g.m * g.n;
+        unsigned blocks = (unsigned)std::min<size_t>((mn + 255) / 256, 4096);
+        splitk_reduce_kernel<EPI><<<blocks, 256, 0, s>>>(splits, (int)g.m, (int)g.n, ep);
+        return hipGetLastError();
+    }
 }
 
 }  // namespace
@@ -243,7 +386,7 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs &g) {
         case Epi::Store: return dispatch<Epi::Store>(s, g, ep);
         case Epi::Gelu: return dispatch<Epi::Gelu>(s, g, ep);
         case Epi::Residual: return dispatch<Epi::Residual>(s, g, ep);
-        case Epi::Qkv: return run<64, 128, 2, 2, Epi::Qkv>(s, g, ep);
+        case Epi::Qkv: return dispatch<Epi::Qkv>(s, g, ep);
     }
     return hipErrorInvalidValue;
 }

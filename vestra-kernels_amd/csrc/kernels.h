@@ -70,6 +70,9 @@ struct GemmArgs {
     float *q, *k_out, *v;
     size_t tokens, heads;
     const float *rot;
+    // split-K workspace (>= splits * m * n floats) or null (no split)
+    float *ws;
+    size_t ws_floats;
 };
 hipError_t launch_gemm(hipStream_t s, const GemmArgs &g);
 

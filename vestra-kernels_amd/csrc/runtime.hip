@@ -23,6 +23,27 @@
 
 #include "kernels.h"
 
+#define NEED(p, what) \
+    do {              \
+        if (!(p)) return null_arg(what); \
+    } while (0)
+
+#define TRY(expr)                   \
+    do {                            \
+        vh_status st_ = (expr);     \
+        if (st_ != VH_OK) return st_; \
+    } while (0)
+
+#define GUARD_BEGIN try {
+#define GUARD_END                                                              \
+    }                                                                          \
+    catch (const std::bad_alloc &) {                                           \
+        return fail(VH_ERR_UPLOAD, "host allocation failed");                 \
+    }                                                                          \
+    catch (...) {                                                              \
+        return fail(VH_ERR_KERNEL, "unexpected host exception");             \
+    }
+
 namespace {
 
 thread_local std::string g_err;
@@ -61,6 +82,8 @@ struct RtState {
     std::map<std::string, float *> rope_cache;  // host-built sin/cos tables
     float *ws = nullptr;                        // grow-only block workspace
     size_t ws_floats = 0;
+    float *sk = nullptr;                        // grow-only split-K partials
+    size_t sk_floats = 0;
     bool profile = false;
     std::vector<ProfileRec> pending;
     std::map<std::string, std::pair<unsigned long long, double>> totals;
@@ -72,6 +95,7 @@ struct RtState {
         hipStreamSynchronize(stream);
         for (auto &kv : rope_cache) hipFree(kv.second);
         if (ws) hipFree(ws);
+        if (sk) hipFree(sk);
         for (auto &p : pending) {
             hipEventDestroy(p.a);
             hipEventDestroy(p.b);
@@ -281,6 +305,28 @@ vh_status workspace(RtState &s, size_t floats, float **out) {
     return VH_OK;
 }
 
+// Split-K partial tiles for the narrow (N <= 1024) projections: up to 8
+// splits of an m x n output.
+constexpr size_t kMaxSplits = 8;
+vh_status splitk_workspace(RtState &s, size_t m, size_t n, float **out, size_t *floats) {
+    *out = nullptr;
+    *floats = 0;
+    if (n > 1024) return VH_OK;
+    const size_t need = kMaxSplits * m * n;
+    if (s.sk_floats < need) {
+        hipStreamSynchronize(s.stream);
+        if (s.sk) hipFree(s.sk);
+        s.sk = nullptr;
+        s.sk_floats = 0;
+        hipError_t e = hipMalloc(&s.sk, need * sizeof(float));
+        if (e != hipSuccess) return fail(VH_ERR_UPLOAD, hip_msg("split-K workspace allocation", e));
+        s.sk_floats = need;
+    }
+    *out = s.sk;
+    *floats = s.sk_floats;
+    return VH_OK;
+}
+
 vh_status prepare_lin(RtState &s, size_t K, size_t N, const float *w, const float *bias,
                       const float *gamma, Lin *L) {
     float *tmp = nullptr;
@@ -315,6 +361,7 @@ vh_status run_lin(RtState &s, const Lin &L, const float *in, size_t rows, vh::Ep
     g.c = c;
     g.bias = L.bias;
     g.gamma = epi == vh::Epi::Gelu ? nullptr : L.gamma;
+    TRY(splitk_workspace(s, rows, L.N, &g.ws, &g.ws_floats));
     return launch(s, name, [&] { return vh::launch_gemm(s.stream, g); });
 }
 
@@ -336,27 +383,6 @@ vh_status run_qkv(RtState &s, const Lin &L, const float *in, size_t images, size
     g.rot = rot;
     return launch(s, "gemm_qkv_rope", [&] { return vh::launch_gemm(s.stream, g); });
 }
-
-#define NEED(p, what) \
-    do {              \
-        if (!(p)) return null_arg(what); \
-    } while (0)
-
-#define TRY(expr)                   \
-    do {                            \
-        vh_status st_ = (expr);     \
-        if (st_ != VH_OK) return st_; \
-    } while (0)
-
-#define GUARD_BEGIN try {
-#define GUARD_END                                                              \
-    }                                                                          \
-    catch (const std::bad_alloc &) {                                           \
-        return fail(VH_ERR_UPLOAD, "host allocation failed");                 \
-    }                                                                          \
-    catch (...) {                                                              \
-        return fail(VH_ERR_KERNEL, "unexpected host exception");             \
-    }
 
 bool mul_overflows(size_t a, size_t b, size_t *out) { return __builtin_mul_overflow(a, b, out); }
 
