@@ -42,8 +42,9 @@ def test_block_config3_vs_oracle(rt, layerscale):
 
 
 def test_block_batch_images_match_single_image_runs(rt):
-    """Images of a batch are independent: the batched launch must equal the
-    per-image oracle and per-image GPU runs."""
+    """Images of a batch are independent: the batched launch matches the
+    per-image oracle and a per-image GPU run (tile and split choices depend on
+    the batch, so the summation order and hence the last bits may differ)."""
     T, B = 865, 2
     w = da3.block_weights(seed=4)
     x = seeded.normal(400, B * T * 768)
@@ -56,7 +57,7 @@ def test_block_batch_images_match_single_image_runs(rt):
     assert max_rel(got, exp) <= BLOCK_TOL
     single = rt.upload_f32(x[T * 768:])
     rt.vit_block_run(blk, single, 1, T, pos)
-    assert np.array_equal(rt.download_f32(single), got[T * 768:])
+    assert max_rel(rt.download_f32(single), got[T * 768:]) <= 1e-6
 
 
 def test_block_no_rope_and_odd_tokens(rt):

@@ -16,6 +16,8 @@
 //
 // attention_online_kernel: the reference device kernel's contract
 // (src/cuda.rs:153-194): any head_dim <= 64, one thread per (head, query).
+#include <cstdlib>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -28,38 +30,62 @@ constexpr int BKV = 64;
 constexpr int LDP = D + 4;  // padded LDS row of a K/V panel
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <bool TOKEN_MAJOR>
-__global__ __launch_bounds__(256) void flash_kernel(const float *__restrict__ Q,
-                                                    const float *__restrict__ K,
-                                                    const float *__restrict__ V,
-                                                    float *__restrict__ O, int T, int heads) {
-    __shared__ __attribute__((aligned(16))) float Ks[2][BKV * LDP];
-    __shared__ __attribute__((aligned(16))) float Vs[2][BKV * LDP];
+struct FlashArgs {
+    const float *q, *k, *v;
+    float *out;
+    int T, heads, bh, qtiles;
+    int xcd_map;  // 1: place all q-tiles of a head on one XCD's L2
+};
+
+// KVS key-panel streams per workgroup: waves [s*4, s*4+4) take the panels
+// p = s (mod KVS) for the same 64 queries, so a SIMD runs KVS waves whose
+// MFMA and softmax phases overlap; the streams merge through LDS at the end.
+template <bool TOKEN_MAJOR, int KVS>
+__global__ __launch_bounds__(256 * KVS) void flash_kernel(FlashArgs fa) {
+    constexpr int NT = 256 * KVS;
+    constexpr int STAGE = KVS * BKV * LDP;  // floats of one K (or V) stage
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float *Ks = smem;              // [2][KVS][BKV*LDP]
+    float *Vs = smem + 2 * STAGE;  // [2][KVS][BKV*LDP]
+
+    // Hardware deals workgroups round-robin over the 8 XCDs; with xcd_map the
+    // items are renumbered so that the q-tiles of one head share an XCD.
+    const int total = fa.bh * fa.qtiles;
+    int item = blockIdx.x;
+    if (fa.xcd_map) {
+        const int per_xcd = (total + 7) / 8;
+        item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+        if (item >= total) return;
+    }
+    const int qt = item % fa.qtiles;
+    const int bh = item / fa.qtiles;
+    const int T = fa.T;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lh = lane >> 4;
-    const int bh = blockIdx.y;
-    const int q0 = blockIdx.x * BQ;
+    const int qgroup = wave & 3, stream = wave >> 2;
+    const int q0 = qt * BQ;
     const size_t head_off = (size_t)bh * T * D;
-    const float *Qh = Q + head_off;
-    const float *Kh = K + head_off;
-    const float *Vh = V + head_off;
+    const float *Qh = fa.q + head_off;
+    const float *Kh = fa.k + head_off;
+    const float *Vh = fa.v + head_off;
 
     // This lane's query (column of S^T) and its Q fragment for all 64 dims:
     // qf[c][s] = Q[query][16c + 4*lh + s].
-    const int query = q0 + wave * 16 + li;
+    const int query = q0 + qgroup * 16 + li;
     f32x4 qf[4];
 #pragma unroll
     for (int c = 0; c < 4; c++)
         qf[c] = query < T ? *reinterpret_cast<const f32x4 *>(Qh + (size_t)query * D + 16 * c + 4 * lh)
                           : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Panel staging: 64 keys x 16 float4 = 1024 chunks, 4 per thread.
-    f32x4 rk[4], rv[4];
+    // One step stages KVS consecutive panels: KVS x 64 keys x 16 float4.
+    constexpr int CH = KVS * BKV * 16 / NT;  // float4 chunks per thread (= 4)
+    f32x4 rk[CH], rv[CH];
     auto gload = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int c = tid + i * 256, key = c >> 4, d4 = (c & 15) * 4;
+        for (int i = 0; i < CH; i++) {
+            int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;  // key in [0, KVS*64)
             int gk = k0 + key;
             if (gk < T) {
                 rk[i] = *reinterpret_cast<const f32x4 *>(Kh + (size_t)gk * D + d4);
@@ -72,10 +98,10 @@ __global__ __launch_bounds__(256) void flash_kernel(const float *__restrict__ Q,
     };
     auto lstore = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int c = tid + i * 256, key = c >> 4, d4 = (c & 15) * 4;
-            *reinterpret_cast<f32x4 *>(&Ks[buf][key * LDP + d4]) = rk[i];
-            *reinterpret_cast<f32x4 *>(&Vs[buf][key * LDP + d4]) = rv[i];
+        for (int i = 0; i < CH; i++) {
+            int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
+            *reinterpret_cast<f32x4 *>(&Ks[buf * STAGE + key * LDP + d4]) = rk[i];
+            *reinterpret_cast<f32x4 *>(&Vs[buf * STAGE + key * LDP + d4]) = rv[i];
         }
     };
 
@@ -86,18 +112,18 @@ __global__ __launch_bounds__(256) void flash_kernel(const float *__restrict__ Q,
 #pragma unroll
     for (int i = 0; i < 4; i++) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int panels = (T + BKV - 1) / BKV;
+    const int steps = (T + KVS * BKV - 1) / (KVS * BKV);
     gload(0);
     lstore(0);
     __syncthreads();
-    for (int p = 0; p < panels; p++) {
-        const int cur = p & 1;
-        const int k0 = p * BKV;
-        const bool next = p + 1 < panels;
-        if (next) gload(k0 + BKV);
+    for (int step = 0; step < steps; step++) {
+        const int cur = step & 1;
+        const int k0 = step * KVS * BKV + stream * BKV;  // this stream's panel
+        const bool next = step + 1 < steps;
+        if (next) gload((step + 1) * KVS * BKV);
 
-        const float *ks = Ks[cur];
-        const float *vs = Vs[cur];
+        const float *ks = Ks + cur * STAGE + stream * BKV * LDP;
+        const float *vs = Vs + cur * STAGE + stream * BKV * LDP;
         // S^T fragments: s[g][r] = S[key 16g+4lh+r][query li].
         f32x4 s[4];
 #pragma unroll
@@ -124,13 +150,16 @@ __global__ __launch_bounds__(256) void flash_kernel(const float *__restrict__ Q,
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float mnew = fmaxf(m, mx);
-        const float corr = __builtin_amdgcn_exp2f(m - mnew);
+        // A stream whose panels so far hold no valid key keeps m = -inf; use
+        // 0 as the reference so exp2 sees -inf (giving 0), never NaN.
+        const float mref = mnew == -INFINITY ? 0.0f : mnew;
+        const float corr = __builtin_amdgcn_exp2f(m - mref);
         float psum = 0.0f;
 #pragma unroll
         for (int g = 0; g < 4; g++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                float pv = __builtin_amdgcn_exp2f(s[g][r] - mnew);
+                float pv = __builtin_amdgcn_exp2f(s[g][r] - mref);
                 s[g][r] = pv;
                 psum += pv;
             }
@@ -153,20 +182,73 @@ __global__ __launch_bounds__(256) void flash_kernel(const float *__restrict__ Q,
         __syncthreads();
     }
 
+    if constexpr (KVS > 1) {
+        // Streams 1.. publish (m, l, o) through LDS; stream 0 merges them in
+        // stream order.  The staging buffers are free after the last barrier.
+        constexpr int REC = 18;  // m, l, 16 outputs per lane
+        float *xbuf = smem;
+        if (stream > 0) {
+            float *rec = xbuf + (((stream - 1) * 4 + qgroup) * 64 + lane) * REC;
+            rec[0] = m;
+            rec[1] = l;
+#pragma unroll
+            for (int df = 0; df < 4; df++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) rec[2 + 4 * df + r] = o[df][r];
+        }
+        __syncthreads();
+        if (stream > 0) return;
+        float mm = m;
+#pragma unroll
+        for (int sidx = 1; sidx < KVS; sidx++)
+            mm = fmaxf(mm, xbuf[(((sidx - 1) * 4 + qgroup) * 64 + lane) * REC]);
+        const float w0 = __builtin_amdgcn_exp2f(m - mm);
+        l *= w0;
+#pragma unroll
+        for (int df = 0; df < 4; df++) o[df] *= w0;
+#pragma unroll
+        for (int sidx = 1; sidx < KVS; sidx++) {
+            const float *rec = xbuf + (((sidx - 1) * 4 + qgroup) * 64 + lane) * REC;
+            const float w = __builtin_amdgcn_exp2f(rec[0] - mm);
+            l += w * rec[1];
+#pragma unroll
+            for (int df = 0; df < 4; df++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) o[df][r] += w * rec[2 + 4 * df + r];
+        }
+    }
+
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
     if (query >= T) return;
     const float inv = 1.0f / l;
     float *orow;
     if constexpr (TOKEN_MAJOR) {
-        const int img = bh / heads, head = bh % heads;
-        orow = O + ((size_t)img * T + query) * ((size_t)heads * D) + (size_t)head * D;
+        const int img = bh / fa.heads, head = bh % fa.heads;
+        orow = fa.out + ((size_t)img * T + query) * ((size_t)fa.heads * D) + (size_t)head * D;
     } else {
-        orow = O + head_off + (size_t)query * D;
+        orow = fa.out + head_off + (size_t)query * D;
     }
 #pragma unroll
     for (int df = 0; df < 4; df++)
         *reinterpret_cast<f32x4 *>(orow + 16 * df + 4 * lh) = o[df] * inv;
+}
+
+template <bool TOKEN_MAJOR, int KVS>
+hipError_t run_flash(hipStream_t s, const FlashArgs &fa) {
+    constexpr size_t lds = 4 * (size_t)KVS * BKV * LDP * sizeof(float);
+    auto kernel = flash_kernel<TOKEN_MAJOR, KVS>;
+    static bool configured = false;
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    const int total = fa.bh * fa.qtiles;
+    const int grid = fa.xcd_map ? (total + 7) / 8 * 8 : total;
+    kernel<<<grid, 256 * KVS, lds, s>>>(fa);
+    return hipGetLastError();
 }
 
 // src/cuda.rs:153-194 contract: one thread per (head, query), 64-key tiles.
@@ -215,12 +297,24 @@ hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k,
                                   float *out, size_t bh, size_t tokens, size_t heads,
                                   bool token_major) {
     if (bh == 0 || tokens == 0) return hipSuccess;
-    dim3 grid((unsigned)((tokens + BQ - 1) / BQ), (unsigned)bh);
-    if (token_major)
-        flash_kernel<true><<<grid, 256, 0, s>>>(q, k, v, out, (int)tokens, (int)heads);
-    else
-        flash_kernel<false><<<grid, 256, 0, s>>>(q, k, v, out, (int)tokens, (int)heads);
-    return hipGetLastError();
+    FlashArgs fa{};
+    fa.q = q;
+    fa.k = k;
+    fa.v = v;
+    fa.out = out;
+    fa.T = (int)tokens;
+    fa.heads = (int)heads;
+    fa.bh = (int)bh;
+    fa.qtiles = (int)((tokens + BQ - 1) / BQ);
+    fa.xcd_map = 1;
+    if (const char *e = std::getenv("VESTRA_HIP_FLASH_XCD")) fa.xcd_map = std::atoi(e) != 0;
+    // Two key streams per workgroup while the grid alone cannot give every
+    // SIMD two waves (VESTRA_HIP_FLASH_STREAMS overrides: 1 or 2).
+    int streams = fa.bh * fa.qtiles < 512 ? 2 : 1;
+    if (const char *e = std::getenv("VESTRA_HIP_FLASH_STREAMS")) streams = std::atoi(e) == 2 ? 2 : 1;
+    if (streams == 2)
+        return token_major ? run_flash<true, 2>(s, fa) : run_flash<false, 2>(s, fa);
+    return token_major ? run_flash<true, 1>(s, fa) : run_flash<false, 1>(s, fa);
 }
 
 hipError_t launch_attention_online(hipStream_t s, const float *q, const float *k,

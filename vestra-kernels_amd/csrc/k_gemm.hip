@@ -54,7 +54,10 @@ __device__ __forceinline__ void epilogue_store(const EpiArgs &ep, size_t idx, in
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT>
+// EXACT: K and the split length are multiples of BK and K % 4 == 0, so every
+// k-slice is whole; rows past M load a clamped in-range row and are zeroed,
+// which keeps the load path branch-free.
+template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__restrict__ A,
                                                               const float *__restrict__ Bt,
                                                               int M, int N, int K,
@@ -86,6 +89,23 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
 
     f32x4 ra[ACH], rb[BCH];
     auto gload = [&](int k0) {
+        if constexpr (EXACT) {
+#pragma unroll
+            for (int i = 0; i < ACH; i++) {
+                int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
+                int gm = m0 + row;
+                f32x4 v = *reinterpret_cast<const f32x4 *>(A + (size_t)min(gm, M - 1) * K + k0 + kq);
+                ra[i] = gm < M ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int i = 0; i < BCH; i++) {
+                int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
+                int gn = n0 + row;
+                f32x4 v = *reinterpret_cast<const f32x4 *>(Bt + (size_t)min(gn, N - 1) * K + k0 + kq);
+                rb[i] = gn < N ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
             int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
@@ -136,26 +156,32 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // Fragments of k-step kk+16 are read from LDS while the MFMAs of k-step
+    // kk run (register double buffering).
     auto compute = [&](int buf) {
-        const float *as = As + buf * BM * LDK;
-        const float *bs = Bs + buf * BN * LDK;
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 16) {
-            f32x4 a[FM], b[FN];
+        const float *as = As + buf * BM * LDK + (wm * TM + li) * LDK + 4 * lh;
+        const float *bs = Bs + buf * BN * LDK + (wn * TN + li) * LDK + 4 * lh;
+        f32x4 a[2][FM], b[2][FN];
+        auto fetch = [&](int slot, int kk) {
 #pragma unroll
             for (int i = 0; i < FM; i++)
-                a[i] = *reinterpret_cast<const f32x4 *>(
-                    &as[(wm * TM + i * 16 + li) * LDK + kk + 4 * lh]);
+                a[slot][i] = *reinterpret_cast<const f32x4 *>(&as[i * 16 * LDK + kk]);
 #pragma unroll
             for (int j = 0; j < FN; j++)
-                b[j] = *reinterpret_cast<const f32x4 *>(
-                    &bs[(wn * TN + j * 16 + li) * LDK + kk + 4 * lh]);
+                b[slot][j] = *reinterpret_cast<const f32x4 *>(&bs[j * 16 * LDK + kk]);
+        };
+        fetch(0, 0);
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 16) {
+            const int cur = (kk / 16) & 1;
+            if (kk + 16 < BK) fetch(cur ^ 1, kk + 16);
 #pragma unroll
             for (int s = 0; s < 4; s++)
 #pragma unroll
                 for (int i = 0; i < FM; i++)
 #pragma unroll
-                    for (int j = 0; j < FN; j++) acc[i][j] = mfma16x16x4(a[i][s], b[j][s], acc[i][j]);
+                    for (int j = 0; j < FN; j++)
+                        acc[i][j] = mfma16x16x4(a[cur][i][s], b[cur][j][s], acc[i][j]);
         }
     };
 
@@ -244,11 +270,29 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     }
 }
 
-// Sums the split-K partials in split order, then applies the epilogue.
+// Sums the split-K partials in split order, then applies the epilogue; four
+// consecutive outputs per thread (N % 4 == 0) so every access is a 16-byte
+// vector.
 template <Epi EPI>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(int splits, int M, int N, EpiArgs ep) {
     const size_t mn = (size_t)M * N;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
+    if ((N & 3) == 0) {
+        const f32x4 *part = reinterpret_cast<const f32x4 *>(ep.partial);
+        for (size_t i4 = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i4 < mn / 4; i4 += stride) {
+            f32x4 v = part[i4];
+            for (int s = 1; s < splits; s++) {
+                const f32x4 w = part[(size_t)s * (mn / 4) + i4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = add_rn(v[e], w[e]);
+            }
+            const size_t idx = i4 * 4;
+            const int col = (int)(idx % N);
+#pragma unroll
+            for (int e = 0; e < 4; e++) epilogue_store<EPI>(ep, idx + e, col + e, v[e]);
+        }
+        return;
+    }
     for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < mn; idx += stride) {
         float v = ep.partial[idx];
         for (int s = 1; s < splits; s++) v = add_rn(v, ep.partial[(size_t)s * mn + idx]);
@@ -260,10 +304,10 @@ struct Tile {
     int bm, bn, bk, wm, wn;
 };
 
-template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT>
-hipError_t run_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int splits) {
+template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT>
+hipError_t launch_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int splits, int kps) {
     constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 4) * sizeof(float);
-    auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, SPLIT>;
+    auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, SPLIT, EXACT>;
     static bool configured = false;
     if (!configured) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
@@ -271,10 +315,17 @@ hipError_t run_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int spl
         if (e != hipSuccess) return e;
         configured = true;
     }
-    const int kps = (int)(((g.k + splits - 1) / splits + BK - 1) / BK * BK);
     dim3 grid((unsigned)((g.n + BN - 1) / BN), (unsigned)((g.m + BM - 1) / BM), (unsigned)splits);
     kernel<<<grid, WM * WN * 64, lds, s>>>(g.a, g.bt, (int)g.m, (int)g.n, (int)g.k, kps, ep);
     return hipGetLastError();
+}
+
+template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT>
+hipError_t run_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int splits) {
+    const int kps = (int)(((g.k + splits - 1) / splits + BK - 1) / BK * BK);
+    const bool exact = g.k % BK == 0 && (size_t)kps * splits == g.k;
+    if (exact) return launch_tile<BM, BN, BK, WM, WN, EPI, SPLIT, true>(s, g, ep, splits, kps);
+    return launch_tile<BM, BN, BK, WM, WN, EPI, SPLIT, false>(s, g, ep, splits, kps);
 }
 
 template <Epi EPI, bool SPLIT>
@@ -286,14 +337,15 @@ hipError_t run_cfg(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, const Ti
     }
     VH_TILE(64, 128, 32, 2, 2)
     VH_TILE(64, 64, 32, 2, 2)
-    VH_TILE(128, 128, 32, 2, 2)
     VH_TILE(64, 128, 32, 2, 4)
     VH_TILE(32, 128, 32, 1, 4)
-    VH_TILE(32, 64, 32, 2, 2)
-    VH_TILE(64, 128, 64, 2, 2)
-    VH_TILE(128, 64, 32, 2, 2)
-    VH_TILE(64, 64, 64, 2, 2)
     VH_TILE(128, 128, 32, 2, 4)
+    VH_TILE(64, 128, 64, 2, 4)
+    VH_TILE(32, 128, 64, 1, 4)
+    VH_TILE(128, 128, 64, 2, 4)
+    VH_TILE(64, 64, 64, 2, 2)
+    VH_TILE(64, 256, 32, 2, 4)
+    VH_TILE(128, 64, 32, 4, 2)
 #undef VH_TILE
     return hipErrorInvalidValue;
 }
@@ -319,22 +371,16 @@ void default_tile(const GemmArgs &g, Tile *t, int *splits) {
     const bool narrow = g.n <= 1024;
     if (g.m <= 1024) {
         if (narrow) {
-            *t = Tile{64, 128, 32, 2, 4};
+            *t = Tile{64, 64, 64, 2, 2};
             *splits = g.k >= 384 ? 3 : 1;
         } else if (g.epi == Epi::Qkv || g.n < 3072) {
-            *t = Tile{64, 128, 32, 2, 4};
+            *t = Tile{64, 64, 64, 2, 2};
         } else {
-            *t = Tile{32, 128, 32, 1, 4};
+            *t = Tile{64, 64, 32, 2, 2};
         }
     } else {
-        if (narrow) {
-            *t = Tile{128, 128, 32, 2, 4};
-            *splits = g.k >= 384 ? 3 : 1;
-        } else if (g.epi == Epi::Qkv || g.n < 3072) {
-            *t = Tile{128, 128, 32, 2, 4};
-        } else {
-            *t = Tile{64, 128, 32, 2, 4};
-        }
+        *t = Tile{128, 128, 32, 2, 4};
+        if (narrow) *splits = g.k >= 384 ? 3 : 1;
     }
 }
 
@@ -360,7 +406,8 @@ hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
         hipError_t e = run_cfg<EPI, true>(s, g, ep, t, splits);
         if (e != hipSuccess) return e;
         size_t mn = g.m * g.n;
-        unsigned blocks = (unsigned)std::min<size_t>((mn + 255) / 256, 4096);
+        unsigned blocks = (unsigned)std::min<size_t>((mn / 4 + 255) / 256, 4096);
+        if (blocks == 0) blocks = 1;
         splitk_reduce_kernel<EPI><<<blocks, 256, 0, s>>>(splits, (int)g.m, (int)g.n, ep);
         return hipGetLastError();
     }

@@ -84,6 +84,7 @@ struct RtState {
     size_t ws_floats = 0;
     float *sk = nullptr;                        // grow-only split-K partials
     size_t sk_floats = 0;
+
     bool profile = false;
     std::vector<ProfileRec> pending;
     std::map<std::string, std::pair<unsigned long long, double>> totals;
@@ -96,6 +97,7 @@ struct RtState {
         for (auto &kv : rope_cache) hipFree(kv.second);
         if (ws) hipFree(ws);
         if (sk) hipFree(sk);
+
         for (auto &p : pending) {
             hipEventDestroy(p.a);
             hipEventDestroy(p.b);
@@ -325,6 +327,13 @@ vh_status splitk_workspace(RtState &s, size_t m, size_t n, float **out, size_t *
     *out = s.sk;
     *floats = s.sk_floats;
     return VH_OK;
+}
+
+vh_status flash(RtState &s, const float *q, const float *k, const float *v, float *out,
+                size_t bh, size_t tokens, size_t heads, bool token_major) {
+    return launch(s, "flash_attention", [&] {
+        return vh::launch_flash_attention(s.stream, q, k, v, out, bh, tokens, heads, token_major);
+    });
 }
 
 vh_status prepare_lin(RtState &s, size_t K, size_t N, const float *w, const float *bias,
@@ -772,10 +781,7 @@ extern "C" vh_status vh_attention_online_f32(const vh_runtime *rt, const vh_tens
     TRY(new_tensor(rt->s, expected, &t, "attention output allocation"));
     vh_status st;
     if (head_dim == 64) {
-        st = launch(s, "flash_attention", [&] {
-            return vh::launch_flash_attention(s.stream, q->ptr, k->ptr, v->ptr, t->ptr, heads,
-                                              tokens, heads, false);
-        });
+        st = flash(s, q->ptr, k->ptr, v->ptr, t->ptr, heads, tokens, heads, false);
     } else {
         const float scale = 1.0f / sqrtf((float)head_dim);
         st = launch(s, "attention_online", [&] {
@@ -812,10 +818,7 @@ extern "C" vh_status vh_flash_attention_f32_da3_base(const vh_runtime *rt, const
     TRY(set_device(s));
     vh_tensor *t = nullptr;
     TRY(new_tensor(rt->s, expected, &t, "attention output allocation"));
-    vh_status st = launch(s, "flash_attention", [&] {
-        return vh::launch_flash_attention(s.stream, q->ptr, k->ptr, v->ptr, t->ptr, heads, tokens,
-                                          heads, token_major != 0);
-    });
+    vh_status st = flash(s, q->ptr, k->ptr, v->ptr, t->ptr, heads, tokens, heads, token_major != 0);
     if (st) {
         delete t;
         return st;
@@ -1411,9 +1414,7 @@ vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size
         return vh::launch_layernorm(s.stream, x, b.ln1_g, b.ln1_b, h, M, D, eps);
     }));
     TRY(run_qkv(s, b.qkv, h, images, tokens, kHeads, rot, q, k, v));
-    TRY(launch(s, "flash_attention", [&] {
-        return vh::launch_flash_attention(s.stream, q, k, v, att, images * kHeads, tokens, kHeads, true);
-    }));
+    TRY(flash(s, q, k, v, att, images * kHeads, tokens, kHeads, true));
     TRY(run_lin(s, b.proj, att, M, vh::Epi::Residual, x, "gemm_proj_residual"));
     TRY(launch(s, "layernorm", [&] {
         return vh::launch_layernorm(s.stream, x, b.ln2_g, b.ln2_b, h, M, D, eps);
