@@ -3,7 +3,8 @@
 // flash_kernel: DA3 head_dim 64, scale 1/8, fp32 MFMA.  A workgroup of four
 // wave64s owns 64 queries of one (image, head); wave w owns queries
 // q0+16w..q0+16w+15.  Key/value panels of 64 keys stream through LDS
-// (double-buffered, rows padded to 68 floats).  Per panel each wave computes
+// (double-buffered; K rows padded to 68 floats, V stored transposed and
+// swizzled).  Per panel each wave computes
 //     S^T[key][query] = K[key][:] . Q[query][:]     (v_mfma_f32_16x16x4_f32)
 // so that register r of lane l holds key 16g+4(l/16)+r of query l%16 --
 // exactly the B-operand layout of the second contraction
@@ -37,16 +38,28 @@ struct FlashArgs {
     int xcd_map;  // 1: place all q-tiles of a head on one XCD's L2
 };
 
+// V panels are stored transposed, Vt[d][key], so that the four keys a lane
+// feeds to one PV k-step are one 16-byte read.  Key column k of row d sits
+// at k ^ vswz(d): the XOR moves whole aligned 4-key groups, and it spreads
+// both the transposing stores (a wave writes 16 d-rows x 4 keys) and the
+// fragment reads (a 16-lane group reads 16 d-rows) over all 64 banks.
+__device__ __forceinline__ int vswz(int d) { return 4 * ((d & 15) ^ ((d >> 2) & 15)); }
+
 // KVS key-panel streams per workgroup: waves [s*4, s*4+4) take the panels
 // p = s (mod KVS) for the same 64 queries, so a SIMD runs KVS waves whose
 // MFMA and softmax phases overlap; the streams merge through LDS at the end.
+// LDS holds one workgroup per CU at KVS = 2 (two at KVS = 1), i.e. two waves
+// per SIMD either way; telling the compiler so lets it keep a panel's
+// fragments in registers instead of trading latency for occupancy.
 template <bool TOKEN_MAJOR, int KVS>
-__global__ __launch_bounds__(256 * KVS) void flash_kernel(FlashArgs fa) {
+__global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2))) void flash_kernel(
+    FlashArgs fa) {
     constexpr int NT = 256 * KVS;
-    constexpr int STAGE = KVS * BKV * LDP;  // floats of one K (or V) stage
+    constexpr int KSTAGE = KVS * BKV * LDP;  // floats of one K stage
+    constexpr int VSTAGE = KVS * D * BKV;    // floats of one V^T stage
     extern __shared__ __attribute__((aligned(16))) float smem[];
-    float *Ks = smem;              // [2][KVS][BKV*LDP]
-    float *Vs = smem + 2 * STAGE;  // [2][KVS][BKV*LDP]
+    float *Ks = smem;               // [2][KVS][BKV*LDP]
+    float *Vs = smem + 2 * KSTAGE;  // [2][KVS][D*BKV], transposed and swizzled
 
     // Hardware deals workgroups round-robin over the 8 XCDs; with xcd_map the
     // items are renumbered so that the q-tiles of one head share an XCD.
@@ -80,28 +93,35 @@ __global__ __launch_bounds__(256 * KVS) void flash_kernel(FlashArgs fa) {
                           : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     // One step stages KVS consecutive panels: KVS x 64 keys x 16 float4.
+    // Keys past T load the last key's row (no branch, no select on the
+    // loaded value, so the loads stay in flight across the MFMAs); their
+    // scores are masked to -inf and their V rows are zeroed when stored.
     constexpr int CH = KVS * BKV * 16 / NT;  // float4 chunks per thread (= 4)
     f32x4 rk[CH], rv[CH];
     auto gload = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < CH; i++) {
-            int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;  // key in [0, KVS*64)
-            int gk = k0 + key;
-            if (gk < T) {
-                rk[i] = *reinterpret_cast<const f32x4 *>(Kh + (size_t)gk * D + d4);
-                rv[i] = *reinterpret_cast<const f32x4 *>(Vh + (size_t)gk * D + d4);
-            } else {
-                rk[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                rv[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
+            const int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
+            const size_t row = (size_t)min(k0 + key, T - 1) * D + d4;
+            rk[i] = *reinterpret_cast<const f32x4 *>(Kh + row);
+            rv[i] = *reinterpret_cast<const f32x4 *>(Vh + row);
         }
     };
-    auto lstore = [&](int buf) {
+    auto lstore = [&](int buf, int k0) {
 #pragma unroll
         for (int i = 0; i < CH; i++) {
-            int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
-            *reinterpret_cast<f32x4 *>(&Ks[buf * STAGE + key * LDP + d4]) = rk[i];
-            *reinterpret_cast<f32x4 *>(&Vs[buf * STAGE + key * LDP + d4]) = rv[i];
+            const int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
+            *reinterpret_cast<f32x4 *>(&Ks[buf * KSTAGE + key * LDP + d4]) = rk[i];
+            // Rows past T become +0 through an all-zero bit mask (a select
+            // here is turned into a branch around one of the stores).
+            const unsigned keep = k0 + key < T ? 0xffffffffu : 0u;
+            float *vt = Vs + buf * VSTAGE + (key / BKV) * D * BKV;
+            const int kin = key % BKV;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int d = d4 + e;
+                vt[d * BKV + (kin ^ vswz(d))] = __uint_as_float(__float_as_uint(rv[i][e]) & keep);
+            }
         }
     };
 
@@ -111,31 +131,61 @@ __global__ __launch_bounds__(256 * KVS) void flash_kernel(FlashArgs fa) {
     f32x4 o[4];           // o[df][r] = O[query][16*df + 4*lh + r] (unnormalised)
 #pragma unroll
     for (int i = 0; i < 4; i++) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    int vcol[4];          // swizzle of this lane's V^T rows 16*df + li
+#pragma unroll
+    for (int df = 0; df < 4; df++) vcol[df] = vswz(16 * df + li);
 
     const int steps = (T + KVS * BKV - 1) / (KVS * BKV);
     gload(0);
-    lstore(0);
+    lstore(0, 0);
     __syncthreads();
+    // Branch-free step loop: the last step reloads its own keys into the idle
+    // buffer, which is never read again.
     for (int step = 0; step < steps; step++) {
         const int cur = step & 1;
         const int k0 = step * KVS * BKV + stream * BKV;  // this stream's panel
-        const bool next = step + 1 < steps;
-        if (next) gload((step + 1) * KVS * BKV);
+        const int kn = min(step + 1, steps - 1) * KVS * BKV;
+        gload(kn);
 
-        const float *ks = Ks + cur * STAGE + stream * BKV * LDP;
-        const float *vs = Vs + cur * STAGE + stream * BKV * LDP;
-        // S^T fragments: s[g][r] = S[key 16g+4lh+r][query li].
+        // All K and V fragments of the panel are read up front; the MFMAs
+        // consume them in issue order.
+        const float *ks = Ks + cur * KSTAGE + stream * BKV * LDP + li * LDP + 4 * lh;
+        const float *vt = Vs + cur * VSTAGE + stream * D * BKV;
+        f32x4 kf[4][4], vf[4][4];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                kf[g][c] = *reinterpret_cast<const f32x4 *>(&ks[16 * g * LDP + 16 * c]);
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int df = 0; df < 4; df++)
+                vf[g][df] = *reinterpret_cast<const f32x4 *>(
+                    &vt[(16 * df + li) * BKV + ((16 * g + 4 * lh) ^ vcol[df])]);
+
+        // S^T fragments: s[g][r] = S[key 16g+4lh+r][query li].  The four key
+        // groups are independent accumulation chains; interleaving them keeps
+        // consecutive MFMAs independent (each chain's order is unchanged).
         f32x4 s[4];
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            s[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int g = 0; g < 4; g++) s[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                f32x4 a = *reinterpret_cast<const f32x4 *>(&ks[(16 * g + li) * LDP + 16 * c + 4 * lh]);
+        for (int c = 0; c < 4; c++)
 #pragma unroll
-                for (int st = 0; st < 4; st++) s[g] = mfma16x16x4(a[st], qf[c][st], s[g]);
-            }
+            for (int st = 0; st < 4; st++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) s[g] = mfma16x16x4(kf[g][c][st], qf[c][st], s[g]);
+        // Issue order of this region: the K fragments, the next step's global
+        // loads, then the QK MFMAs with one V fragment read after every four.
+        __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 2 * CH, 0);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
         // Online softmax for this lane's query over its 16 keys of the panel.
         float mx = -INFINITY;
 #pragma unroll
@@ -167,18 +217,25 @@ __global__ __launch_bounds__(256 * KVS) void flash_kernel(FlashArgs fa) {
         m = mnew;
 #pragma unroll
         for (int df = 0; df < 4; df++) o[df] *= corr;
+        __builtin_amdgcn_sched_barrier(0);
         // O^T[d][query] += V^T[d][key] P^T[key][query]: lane supplies
-        // V[16g+4lh+st][16df+li] (A) and s[g][st] (B).
+        // V[16g+4lh+st][16df+li] (A, from vf) and s[g][st] (B).
 #pragma unroll
         for (int g = 0; g < 4; g++)
 #pragma unroll
-            for (int st = 0; st < 4; st++) {
-                const float *vrow = vs + (16 * g + 4 * lh + st) * LDP + li;
+            for (int st = 0; st < 4; st++)
 #pragma unroll
-                for (int df = 0; df < 4; df++) o[df] = mfma16x16x4(vrow[16 * df], s[g][st], o[df]);
-            }
+                for (int df = 0; df < 4; df++) o[df] = mfma16x16x4(vf[g][df][st], s[g][st], o[df]);
 
-        if (next) lstore(cur ^ 1);
+        lstore(cur ^ 1, kn);
+        // The next stage's LDS stores (4 K + 16 transposed V per thread) go
+        // out between the PV MFMAs.
+#pragma unroll
+        for (int i = 0; i < 5 * CH; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 64 - 15 * CH, 0);
         __syncthreads();
     }
 
@@ -236,7 +293,7 @@ __global__ __launch_bounds__(256 * KVS) void flash_kernel(FlashArgs fa) {
 
 template <bool TOKEN_MAJOR, int KVS>
 hipError_t run_flash(hipStream_t s, const FlashArgs &fa) {
-    constexpr size_t lds = 4 * (size_t)KVS * BKV * LDP * sizeof(float);
+    constexpr size_t lds = 2 * (size_t)KVS * (BKV * LDP + D * BKV) * sizeof(float);
     auto kernel = flash_kernel<TOKEN_MAJOR, KVS>;
     static bool configured = false;
     if (!configured) {

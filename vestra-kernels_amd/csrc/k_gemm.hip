@@ -55,8 +55,11 @@ __device__ __forceinline__ void epilogue_store(const EpiArgs &ep, size_t idx, in
 }
 
 // EXACT: K and the split length are multiples of BK and K % 4 == 0, so every
-// k-slice is whole; rows past M load a clamped in-range row and are zeroed,
-// which keeps the load path branch-free.
+// k-slice is whole.  Rows past M (columns past N) load a clamped in-range row
+// and are NOT zeroed: C[m][n] depends only on A row m and Bt row n, and rows
+// or columns past the edge are never stored.  Selecting on the loaded value
+// would make the compiler wait for the prefetch before the MFMAs of the
+// current slice, so the load path stays select-free.
 template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__restrict__ A,
                                                               const float *__restrict__ Bt,
@@ -93,16 +96,12 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
 #pragma unroll
             for (int i = 0; i < ACH; i++) {
                 int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
-                int gm = m0 + row;
-                f32x4 v = *reinterpret_cast<const f32x4 *>(A + (size_t)min(gm, M - 1) * K + k0 + kq);
-                ra[i] = gm < M ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                ra[i] = *reinterpret_cast<const f32x4 *>(A + (size_t)min(m0 + row, M - 1) * K + k0 + kq);
             }
 #pragma unroll
             for (int i = 0; i < BCH; i++) {
                 int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
-                int gn = n0 + row;
-                f32x4 v = *reinterpret_cast<const f32x4 *>(Bt + (size_t)min(gn, N - 1) * K + k0 + kq);
-                rb[i] = gn < N ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                rb[i] = *reinterpret_cast<const f32x4 *>(Bt + (size_t)min(n0 + row, N - 1) * K + k0 + kq);
             }
             return;
         }
@@ -189,13 +188,49 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     gload(kbeg);
     lstore(0);
     __syncthreads();
-    for (int t = 0; t < ktiles; t++) {
-        const int cur = t & 1;
-        const bool next = t + 1 < ktiles;
-        if (next) gload(kbeg + (t + 1) * BK);
-        compute(cur);
-        if (next) lstore(cur ^ 1);
-        __syncthreads();
+    if constexpr (EXACT) {
+        // Branch-free slice loop: the last iteration reloads its own slice
+        // into the idle buffer (never read again), so each iteration is one
+        // basic block and its instruction order can be pinned: the fragment
+        // reads of k-step s+1 and the LDS stores of the next slice issue in
+        // the shadow of the MFMAs of k-step s, and the global loads of the
+        // next slice go out first.
+        for (int t = 0; t < ktiles; t++) {
+            const int cur = t & 1;
+            gload(kbeg + min(t + 1, ktiles - 1) * BK);
+            compute(cur);
+            lstore(cur ^ 1);
+            constexpr int NR = FM + FN, NM = 4 * FM * FN, NL = ACH + BCH;
+            __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);  // k-step 0 fragments
+            __builtin_amdgcn_sched_group_barrier(0x020, NL, 0);  // next slice, global
+#pragma unroll
+            for (int s = 0; s + 1 < BK / 16; s++) {
+#pragma unroll
+                for (int r = 0; r < NR; r++) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
+            }
+            constexpr int NW = NL < NM ? NL : NM;
+#pragma unroll
+            for (int r = 0; r < NW; r++) {
+                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NM - NW, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, NL - NW, 0);
+            __syncthreads();
+        }
+    } else {
+        for (int t = 0; t < ktiles; t++) {
+            const int cur = t & 1;
+            const bool next = t + 1 < ktiles;
+            if (next) gload(kbeg + (t + 1) * BK);
+            compute(cur);
+            if (next) lstore(cur ^ 1);
+            __syncthreads();
+        }
     }
 
     // C fragment layout: register r of lane l holds row 4*(l/16)+r, column l%16.
@@ -226,6 +261,23 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
         float bias[FN];
 #pragma unroll
         for (int j = 0; j < FN; j++) bias[j] = ep.bias[colw + j * 16 + li];
+        // Rotation (sin, cos) of every row this lane stores, read before any
+        // store from clamped rows so that the reads overlap.
+        float2 rot[FM][4][FN / 2];
+        if (rope) {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int t = min(rbase + i * 16 + r, M - 1) % ep.tokens;
+#pragma unroll
+                    for (int h = 0; h < FN / 2; h++) {
+                        const int axis = d0 / 32 + h;
+                        rot[i][r][h] = *reinterpret_cast<const float2 *>(
+                            ep.rot + (((size_t)t * 2 + axis) * 16 + li) * 2);
+                    }
+                }
+        }
 #pragma unroll
         for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -241,9 +293,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                     // each 32-wide axis half sit in fragments (2h, 2h+1).
 #pragma unroll
                     for (int h = 0; h < FN / 2; h++) {
-                        const int axis = d0 / 32 + h;
-                        const float *rr = ep.rot + (((size_t)t * 2 + axis) * 16 + li) * 2;
-                        const float sn = rr[0], cs = rr[1];
+                        const float sn = rot[i][r][h].x, cs = rot[i][r][h].y;
                         const float a = vals[2 * h], b = vals[2 * h + 1];
                         vals[2 * h] = sub_rn(mul_rn(a, cs), mul_rn(b, sn));
                         vals[2 * h + 1] = add_rn(mul_rn(b, cs), mul_rn(a, sn));
@@ -254,7 +304,30 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                 for (int j = 0; j < FN; j++) orow[j * 16 + li] = vals[j];
             }
     } else {
+        // Every global read of the epilogue (bias, gamma, and the residual
+        // for Residual) is issued from a clamped in-range index before any
+        // store, so the reads overlap instead of each waiting behind the
+        // bounds branch of its element.
         const int cbase = n0 + wn * TN + li;
+        float bias[FN], gamma[FN];
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int col = min(cbase + j * 16, N - 1);
+            bias[j] = ep.bias ? ep.bias[col] : 0.0f;
+            gamma[j] = ep.gamma ? ep.gamma[col] : 1.0f;
+        }
+        float resid[EPI == Epi::Residual ? FM : 1][FN][4];
+        if constexpr (EPI == Epi::Residual) {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const size_t row = min(rbase + i * 16 + r, M - 1);
+                        resid[i][j][r] = ep.c[row * N + min(cbase + j * 16, N - 1)];
+                    }
+        }
 #pragma unroll
         for (int j = 0; j < FN; j++) {
             const int col = cbase + j * 16;
@@ -264,7 +337,19 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int row = rbase + i * 16 + r;
-                    if (row < M) epilogue_store<EPI>(ep, (size_t)row * N + col, col, acc[i][j][r]);
+                    if (row >= M) continue;
+                    const size_t idx = (size_t)row * N + col;
+                    float v = acc[i][j][r];
+                    if (ep.bias) v = add_rn(v, bias[j]);
+                    if constexpr (EPI == Epi::Store) {
+                        if (ep.gamma) v = mul_rn(v, gamma[j]);
+                        ep.c[idx] = v;
+                    } else if constexpr (EPI == Epi::Gelu) {
+                        ep.c[idx] = idx < ep.tail_start ? gelu_avx512_form(v) : gelu_scalar_form(v);
+                    } else {
+                        if (ep.gamma) v = mul_rn(v, gamma[j]);
+                        ep.c[idx] = add_rn(resid[i][j][r], v);
+                    }
                 }
         }
     }
@@ -323,7 +408,8 @@ hipError_t launch_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int 
 template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT>
 hipError_t run_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int splits) {
     const int kps = (int)(((g.k + splits - 1) / splits + BK - 1) / BK * BK);
-    const bool exact = g.k % BK == 0 && (size_t)kps * splits == g.k;
+    // K == 0 takes the masked path: the whole-slice loads would touch empty operands.
+    const bool exact = g.k > 0 && g.k % BK == 0 && (size_t)kps * splits == g.k;
     if (exact) return launch_tile<BM, BN, BK, WM, WN, EPI, SPLIT, true>(s, g, ep, splits, kps);
     return launch_tile<BM, BN, BK, WM, WN, EPI, SPLIT, false>(s, g, ep, splits, kps);
 }
@@ -363,24 +449,32 @@ bool tile_override(Tile *t, int *splits) {
     return true;
 }
 
-// Per-shape defaults from the tile sweep on MI355X (DA3 projections at 865
-// and 4 x 865 tokens): eight-wave workgroups, split-K 3 for the N = 768
-// projections so that the grid covers the 256 CUs.
+// Per-shape defaults from the kernel-trace tile sweep on MI355X (DA3
+// projections at 865 and 4 x 865 tokens).  Only the long-K narrow projection
+// (fc2: K = 3072, N = 768) splits K: with K = 768 the 64x64 grid already
+// keeps every CU busy for less time than a separate reduction costs.
 void default_tile(const GemmArgs &g, Tile *t, int *splits) {
     *splits = 1;
     const bool narrow = g.n <= 1024;
+    const bool long_k = g.k >= 2048;
     if (g.m <= 1024) {
-        if (narrow) {
-            *t = Tile{64, 64, 64, 2, 2};
-            *splits = g.k >= 384 ? 3 : 1;
-        } else if (g.epi == Epi::Qkv || g.n < 3072) {
-            *t = Tile{64, 64, 64, 2, 2};
-        } else {
+        if (narrow && long_k) {
+            *t = Tile{64, 128, 64, 2, 4};
+            *splits = 3;
+        } else if (narrow || g.n >= 3072) {
             *t = Tile{64, 64, 32, 2, 2};
+        } else {
+            *t = Tile{64, 128, 64, 2, 4};
         }
     } else {
-        *t = Tile{128, 128, 32, 2, 4};
-        if (narrow) *splits = g.k >= 384 ? 3 : 1;
+        if (narrow && long_k) {
+            *t = Tile{128, 128, 32, 2, 4};
+            *splits = 3;
+        } else if (narrow || g.n >= 3072) {
+            *t = Tile{64, 64, 32, 2, 2};
+        } else {
+            *t = Tile{128, 128, 32, 2, 4};
+        }
     }
 }
 
