@@ -37,7 +37,7 @@ T = 865
 D, H, HD, F = 768, 12, 64, 3072
 FLOPS = {
     "gemm_qkv_rope": 2.0 * T * D * 3 * D,
-    "gemm_proj_residual": 2.0 * T * D * D,
+    "gemm_proj_residual_ln": 2.0 * T * D * D,
     "gemm_fc1_gelu": 2.0 * T * D * F,
     "gemm_fc2_residual": 2.0 * T * F * D,
     "flash_attention": 4.0 * H * T * T * HD,

@@ -94,3 +94,22 @@ def test_encoder_config5b_long_sequence_2_layers(rt):
     layers keep the CPU oracle's generic attention to seconds."""
     got, exp, x = _encoder_case(rt, images=1, rows=48, cols=72, layers=2)
     assert max_rel(got, exp) <= ENCODER_TOL
+
+
+@pytest.mark.parametrize("images, T", [(1, 865), (2, 97)])
+def test_encoder_fused_norms_match_block_by_block_runs(rt, images, T):
+    """Inside the encoder each fc2 reduction also writes the next layer's
+    LayerNorm1 input; block by block, a separate LayerNorm kernel does.  Both
+    round every element the same way, so three layers agree bit for bit."""
+    ws = [da3.block_weights(seed=9, layer=l, layerscale=0.5) for l in range(3)]
+    x = seeded.normal(900 + T, images * T * 768)
+    pos = da3.positions_yx(24, 36) if T == 865 else None
+    blocks = [rt.prepare_block(w) for w in ws]
+    fused = rt.upload_f32(x)
+    rt.encoder_run(blocks, fused, images, T, pos)
+    step = rt.upload_f32(x)
+    for b in blocks:
+        rt.vit_block_run(b, step, images, T, pos)
+    a, b = rt.download_f32(fused), rt.download_f32(step)
+    assert np.isfinite(a).all()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

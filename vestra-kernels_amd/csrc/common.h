@@ -63,6 +63,40 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// LayerNorm of one row held by one wave in registers: r[j] = the float4
+// chunk lane + 64 j of the row (n4 = cols / 4 <= 256 chunks; absent chunks
+// are zero).  Mean, then the variance about the mean (two passes over the
+// registers), inv = 1 / sqrt(var + eps) correctly rounded; every kernel that
+// normalises rows this way shares these two functions and so produces the
+// same bits.
+__device__ __forceinline__ void ln_row_stats(const f32x4 (&r)[4], int lane, int n4, int cols,
+                                             float eps, float &mean, float &inv) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) s += (r[j].x + r[j].y) + (r[j].z + r[j].w);
+    mean = div_rn(wave_sum(s), (float)cols);
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (lane + j * 64 < n4) {
+            const f32x4 d = r[j] - mean;
+            q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+        }
+    }
+    const float var = div_rn(wave_sum(q), (float)cols);
+    inv = div_rn(1.0f, sqrt_rn(add_rn(var, eps)));
+}
+// ((x - mean) * inv) * g + b, each step separately rounded.
+__device__ __forceinline__ f32x4 ln_apply(f32x4 x, float mean, float inv, f32x4 g, f32x4 b) {
+    f32x4 o;
+    o.x = add_rn(mul_rn(mul_rn(sub_rn(x.x, mean), inv), g.x), b.x);
+    o.y = add_rn(mul_rn(mul_rn(sub_rn(x.y, mean), inv), g.y), b.y);
+    o.z = add_rn(mul_rn(mul_rn(sub_rn(x.z, mean), inv), g.z), b.z);
+    o.w = add_rn(mul_rn(mul_rn(sub_rn(x.w, mean), inv), g.w), b.w);
+    return o;
+}
+
+
 // Cephes-style exp with the constants and FMA placement of the reference's
 // AVX-512 exp (src/simd_avx512.rs:22-69).  x86 min/max select the second
 // operand on NaN; cvttps truncates toward zero.

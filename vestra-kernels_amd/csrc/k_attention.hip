@@ -36,6 +36,10 @@ struct FlashArgs {
     float *out;
     int T, heads, bh, qtiles;
     int xcd_map;  // 1: place all q-tiles of a head on one XCD's L2
+    // Key split across workgroups: split z takes keys [z*split_keys, ...).
+    int splits, split_keys;
+    float *po;    // [splits][bh][T][64] unnormalised outputs
+    float2 *pml;  // [splits][bh][T] (running max in the base-2 domain, sum)
 };
 
 // V panels are stored transposed, Vt[d][key], so that the four keys a lane
@@ -51,7 +55,10 @@ __device__ __forceinline__ int vswz(int d) { return 4 * ((d & 15) ^ ((d >> 2) & 
 // LDS holds one workgroup per CU at KVS = 2 (two at KVS = 1), i.e. two waves
 // per SIMD either way; telling the compiler so lets it keep a panel's
 // fragments in registers instead of trading latency for occupancy.
-template <bool TOKEN_MAJOR, int KVS>
+//
+// SPLIT: the workgroup covers only the keys of split z and writes its
+// unnormalised output and (max, sum) for flash_merge_kernel.
+template <bool TOKEN_MAJOR, int KVS, bool SPLIT>
 __global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2))) void flash_kernel(
     FlashArgs fa) {
     constexpr int NT = 256 * KVS;
@@ -62,17 +69,23 @@ __global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2)
     float *Vs = smem + 2 * KSTAGE;  // [2][KVS][D*BKV], transposed and swizzled
 
     // Hardware deals workgroups round-robin over the 8 XCDs; with xcd_map the
-    // items are renumbered so that the q-tiles of one head share an XCD.
-    const int total = fa.bh * fa.qtiles;
+    // items are renumbered so that the q-tiles (and key splits) of one head
+    // share an XCD.
+    const int splits = SPLIT ? fa.splits : 1;
+    const int total = fa.bh * fa.qtiles * splits;
     int item = blockIdx.x;
     if (fa.xcd_map) {
         const int per_xcd = (total + 7) / 8;
         item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
         if (item >= total) return;
     }
-    const int qt = item % fa.qtiles;
-    const int bh = item / fa.qtiles;
+    const int z = item % splits;
+    const int qt = (item / splits) % fa.qtiles;
+    const int bh = item / splits / fa.qtiles;
     const int T = fa.T;
+    // This workgroup's keys [kb, ke).
+    const int kb = SPLIT ? z * fa.split_keys : 0;
+    const int ke = SPLIT ? min(T, kb + fa.split_keys) : T;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lh = lane >> 4;
@@ -102,7 +115,7 @@ __global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2)
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
-            const size_t row = (size_t)min(k0 + key, T - 1) * D + d4;
+            const size_t row = (size_t)min(k0 + key, ke - 1) * D + d4;
             rk[i] = *reinterpret_cast<const f32x4 *>(Kh + row);
             rv[i] = *reinterpret_cast<const f32x4 *>(Vh + row);
         }
@@ -114,7 +127,7 @@ __global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2)
             *reinterpret_cast<f32x4 *>(&Ks[buf * KSTAGE + key * LDP + d4]) = rk[i];
             // Rows past T become +0 through an all-zero bit mask (a select
             // here is turned into a branch around one of the stores).
-            const unsigned keep = k0 + key < T ? 0xffffffffu : 0u;
+            const unsigned keep = k0 + key < ke ? 0xffffffffu : 0u;
             float *vt = Vs + buf * VSTAGE + (key / BKV) * D * BKV;
             const int kin = key % BKV;
 #pragma unroll
@@ -135,16 +148,16 @@ __global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2)
 #pragma unroll
     for (int df = 0; df < 4; df++) vcol[df] = vswz(16 * df + li);
 
-    const int steps = (T + KVS * BKV - 1) / (KVS * BKV);
-    gload(0);
-    lstore(0, 0);
+    const int steps = (ke - kb + KVS * BKV - 1) / (KVS * BKV);
+    gload(kb);
+    lstore(0, kb);
     __syncthreads();
     // Branch-free step loop: the last step reloads its own keys into the idle
     // buffer, which is never read again.
     for (int step = 0; step < steps; step++) {
         const int cur = step & 1;
-        const int k0 = step * KVS * BKV + stream * BKV;  // this stream's panel
-        const int kn = min(step + 1, steps - 1) * KVS * BKV;
+        const int k0 = kb + step * KVS * BKV + stream * BKV;  // this stream's panel
+        const int kn = kb + min(step + 1, steps - 1) * KVS * BKV;
         gload(kn);
 
         // All K and V fragments of the panel are read up front; the MFMAs
@@ -193,7 +206,7 @@ __global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int key = k0 + 16 * g + 4 * lh + r;
-                float t = key < T ? s[g][r] * scale : -INFINITY;
+                float t = key < ke ? s[g][r] * scale : -INFINITY;
                 s[g][r] = t;
                 mx = fmaxf(mx, t);
             }
@@ -278,6 +291,14 @@ __global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2)
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
     if (query >= T) return;
+    if constexpr (SPLIT) {
+        const size_t prow = ((size_t)z * fa.bh + bh) * T + query;
+        float *orow = fa.po + prow * D;
+#pragma unroll
+        for (int df = 0; df < 4; df++) *reinterpret_cast<f32x4 *>(orow + 16 * df + 4 * lh) = o[df];
+        if (lh == 0) fa.pml[prow] = make_float2(m, l);
+        return;
+    }
     const float inv = 1.0f / l;
     float *orow;
     if constexpr (TOKEN_MAJOR) {
@@ -291,10 +312,50 @@ __global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2)
         *reinterpret_cast<f32x4 *>(orow + 16 * df + 4 * lh) = o[df] * inv;
 }
 
-template <bool TOKEN_MAJOR, int KVS>
+// Combines the key splits of each (head, query) in split order:
+// O = sum_z 2^(m_z - M) o_z / sum_z 2^(m_z - M) l_z with M = max_z m_z.
+// One thread per four output dims; all reads are issued first.
+template <bool TOKEN_MAJOR, int S>
+__global__ __launch_bounds__(256) void flash_merge_kernel(FlashArgs fa) {
+    const size_t rows = (size_t)fa.bh * fa.T;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= rows * 16) return;
+    const size_t row = idx >> 4;
+    const int d4 = (int)(idx & 15) * 4;
+    float2 ml[S];
+    f32x4 po[S];
+#pragma unroll
+    for (int z = 0; z < S; z++) {
+        ml[z] = fa.pml[z * rows + row];
+        po[z] = *reinterpret_cast<const f32x4 *>(fa.po + (z * rows + row) * D + d4);
+    }
+    float mm = ml[0].x;
+#pragma unroll
+    for (int z = 1; z < S; z++) mm = fmaxf(mm, ml[z].x);
+    float lsum = 0.0f;
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int z = 0; z < S; z++) {
+        const float w = __builtin_amdgcn_exp2f(ml[z].x - mm);
+        lsum += w * ml[z].y;
+        acc += w * po[z];
+    }
+    const float inv = 1.0f / lsum;
+    float *dst;
+    if constexpr (TOKEN_MAJOR) {
+        const int bh = (int)(row / fa.T), query = (int)(row % fa.T);
+        const int img = bh / fa.heads, head = bh % fa.heads;
+        dst = fa.out + ((size_t)img * fa.T + query) * ((size_t)fa.heads * D) + (size_t)head * D;
+    } else {
+        dst = fa.out + row * D;
+    }
+    *reinterpret_cast<f32x4 *>(dst + d4) = acc * inv;
+}
+
+template <bool TOKEN_MAJOR, int KVS, bool SPLIT>
 hipError_t run_flash(hipStream_t s, const FlashArgs &fa) {
     constexpr size_t lds = 2 * (size_t)KVS * (BKV * LDP + D * BKV) * sizeof(float);
-    auto kernel = flash_kernel<TOKEN_MAJOR, KVS>;
+    auto kernel = flash_kernel<TOKEN_MAJOR, KVS, SPLIT>;
     static bool configured = false;
     if (!configured) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
@@ -302,9 +363,17 @@ hipError_t run_flash(hipStream_t s, const FlashArgs &fa) {
         if (e != hipSuccess) return e;
         configured = true;
     }
-    const int total = fa.bh * fa.qtiles;
+    const int total = fa.bh * fa.qtiles * (SPLIT ? fa.splits : 1);
     const int grid = fa.xcd_map ? (total + 7) / 8 * 8 : total;
     kernel<<<grid, 256 * KVS, lds, s>>>(fa);
+    if constexpr (SPLIT) {
+        const size_t threads = (size_t)fa.bh * fa.T * 16;
+        const dim3 grid((unsigned)((threads + 255) / 256));
+        static_assert(kMaxFlashSplits == 4, "merge instantiations");
+        if (fa.splits == 2) flash_merge_kernel<TOKEN_MAJOR, 2><<<grid, 256, 0, s>>>(fa);
+        else if (fa.splits == 3) flash_merge_kernel<TOKEN_MAJOR, 3><<<grid, 256, 0, s>>>(fa);
+        else flash_merge_kernel<TOKEN_MAJOR, 4><<<grid, 256, 0, s>>>(fa);
+    }
     return hipGetLastError();
 }
 
@@ -350,9 +419,13 @@ __global__ void attention_online_kernel(const float *__restrict__ q, const float
 
 }  // namespace
 
+size_t flash_workspace_floats(size_t bh, size_t tokens) {
+    return (size_t)kMaxFlashSplits * bh * tokens * (D + 2);
+}
+
 hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k, const float *v,
                                   float *out, size_t bh, size_t tokens, size_t heads,
-                                  bool token_major) {
+                                  bool token_major, float *ws, size_t ws_floats) {
     if (bh == 0 || tokens == 0) return hipSuccess;
     FlashArgs fa{};
     fa.q = q;
@@ -365,13 +438,57 @@ hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k,
     fa.qtiles = (int)((tokens + BQ - 1) / BQ);
     fa.xcd_map = 1;
     if (const char *e = std::getenv("VESTRA_HIP_FLASH_XCD")) fa.xcd_map = std::atoi(e) != 0;
-    // Two key streams per workgroup while the grid alone cannot give every
-    // SIMD two waves (VESTRA_HIP_FLASH_STREAMS overrides: 1 or 2).
-    int streams = fa.bh * fa.qtiles < 512 ? 2 : 1;
-    if (const char *e = std::getenv("VESTRA_HIP_FLASH_STREAMS")) streams = std::atoi(e) == 2 ? 2 : 1;
+
+    // Layout choice by a per-SIMD load model, in 64-key panels: two key
+    // streams in one workgroup per CU, or one stream with two workgroups per
+    // CU, optionally splitting the keys across workgroups (plus a merge
+    // pass) when the grid alone leaves CUs idle.
+    const long items = (long)fa.bh * fa.qtiles;
+    const long panels = ((long)tokens + BKV - 1) / BKV;
+    auto rounds = [](long wgs, long slots) { return (wgs + slots - 1) / slots; };
+    long best = rounds(items, 256) * panels;
+    int streams = 2, splits = 1;
+    if (rounds(items, 512) * 2 * panels < best) {
+        best = rounds(items, 512) * 2 * panels;
+        streams = 1;
+    }
+    auto split_keys = [&](int sp) { return (int)((panels + sp - 1) / sp) * BKV; };
+    auto usable = [&](int sp) {
+        const long pps = (panels + sp - 1) / sp;
+        return sp >= 2 && sp <= kMaxFlashSplits && (panels + pps - 1) / pps == sp &&
+               ws != nullptr && ws_floats >= (size_t)sp * bh * tokens * (D + 2);
+    };
+    for (int sp = 2; sp <= kMaxFlashSplits; sp++) {
+        if (!usable(sp)) continue;
+        const long cost = rounds(items * sp, 512) * 2 * (split_keys(sp) / BKV) + 1;
+        if (cost < best) {
+            best = cost;
+            splits = sp;
+            streams = 1;
+        }
+    }
+    // Overrides for A/B runs: VESTRA_HIP_FLASH_SPLITS (1 = none) and
+    // VESTRA_HIP_FLASH_STREAMS (1 or 2, unsplit only).
+    if (const char *e = std::getenv("VESTRA_HIP_FLASH_SPLITS")) {
+        const int sp = std::atoi(e);
+        if (sp <= 1) splits = 1;
+        else if (usable(sp)) splits = sp, streams = 1;
+    }
+    if (const char *e = std::getenv("VESTRA_HIP_FLASH_STREAMS"))
+        if (splits == 1) streams = std::atoi(e) == 2 ? 2 : 1;
+
+    if (splits > 1) {
+        fa.splits = splits;
+        fa.split_keys = split_keys(splits);
+        fa.po = ws;
+        fa.pml = reinterpret_cast<float2 *>(ws + (size_t)splits * bh * tokens * D);
+        return token_major ? run_flash<true, 1, true>(s, fa) : run_flash<false, 1, true>(s, fa);
+    }
+    fa.splits = 1;
+    fa.split_keys = (int)tokens;
     if (streams == 2)
-        return token_major ? run_flash<true, 2>(s, fa) : run_flash<false, 2>(s, fa);
-    return token_major ? run_flash<true, 1>(s, fa) : run_flash<false, 1>(s, fa);
+        return token_major ? run_flash<true, 2, false>(s, fa) : run_flash<false, 2, false>(s, fa);
+    return token_major ? run_flash<true, 1, false>(s, fa) : run_flash<false, 1, false>(s, fa);
 }
 
 hipError_t launch_attention_online(hipStream_t s, const float *q, const float *k,

@@ -75,38 +75,20 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float *__restrict_
     if ((cols & 3) == 0 && cols <= 1024 && ((((uintptr_t)x) | ((uintptr_t)y)) & 15) == 0) {
         const int n4 = (int)(cols >> 2);
         f32x4 r[4];
-        float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             int idx = lane + j * 64;
             r[j] = idx < n4 ? reinterpret_cast<const f32x4 *>(x)[idx] : f32x4{0, 0, 0, 0};
-            s += (r[j].x + r[j].y) + (r[j].z + r[j].w);
         }
-        float mean = div_rn(wave_sum(s), (float)cols);
-        float q = 0.0f;
+        float mean, inv;
+        ln_row_stats(r, lane, n4, (int)cols, eps, mean, inv);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             int idx = lane + j * 64;
-            if (idx < n4) {
-                f32x4 d = r[j] - mean;
-                q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
-            }
-        }
-        float var = div_rn(wave_sum(q), (float)cols);
-        float inv = div_rn(1.0f, sqrt_rn(add_rn(var, eps)));
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            int idx = lane + j * 64;
-            if (idx < n4) {
-                f32x4 g = reinterpret_cast<const f32x4 *>(gamma)[idx];
-                f32x4 b = reinterpret_cast<const f32x4 *>(beta)[idx];
-                f32x4 o;
-                o.x = add_rn(mul_rn(mul_rn(sub_rn(r[j].x, mean), inv), g.x), b.x);
-                o.y = add_rn(mul_rn(mul_rn(sub_rn(r[j].y, mean), inv), g.y), b.y);
-                o.z = add_rn(mul_rn(mul_rn(sub_rn(r[j].z, mean), inv), g.z), b.z);
-                o.w = add_rn(mul_rn(mul_rn(sub_rn(r[j].w, mean), inv), g.w), b.w);
-                reinterpret_cast<f32x4 *>(y)[idx] = o;
-            }
+            if (idx < n4)
+                reinterpret_cast<f32x4 *>(y)[idx] =
+                    ln_apply(r[j], mean, inv, reinterpret_cast<const f32x4 *>(gamma)[idx],
+                             reinterpret_cast<const f32x4 *>(beta)[idx]);
         }
     } else {
         float s = 0.0f;

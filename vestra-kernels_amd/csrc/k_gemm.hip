@@ -385,6 +385,105 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(int splits, int M, i
     }
 }
 
+// splitk_reduce_kernel for 2-4 splits and N % 4 == 0: one float4 of outputs
+// per thread, every read (partials, bias, gamma, residual) issued before the
+// arithmetic.  Per element exactly epilogue_store<EPI> of the split-order sum.
+template <Epi EPI, int SPLITS>
+__global__ __launch_bounds__(256) void splitk_reduce4_kernel(int M, int N, EpiArgs ep) {
+    const size_t mn4 = (size_t)M * N / 4;
+    const size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i4 >= mn4) return;
+    const f32x4 *part = reinterpret_cast<const f32x4 *>(ep.partial);
+    const int col = (int)((i4 * 4) % N);
+    f32x4 p[SPLITS];
+#pragma unroll
+    for (int sp = 0; sp < SPLITS; sp++) p[sp] = part[(size_t)sp * mn4 + i4];
+    const f32x4 b = ep.bias ? *reinterpret_cast<const f32x4 *>(ep.bias + col) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const f32x4 g = ep.gamma ? *reinterpret_cast<const f32x4 *>(ep.gamma + col) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+    f32x4 *c4 = reinterpret_cast<f32x4 *>(ep.c) + i4;
+    f32x4 x = EPI == Epi::Residual ? *c4 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 v = p[0];
+#pragma unroll
+    for (int sp = 1; sp < SPLITS; sp++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = add_rn(v[e], p[sp][e]);
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        float t = v[e];
+        if (ep.bias) t = add_rn(t, b[e]);
+        if constexpr (EPI == Epi::Gelu) {
+            o[e] = i4 * 4 + e < ep.tail_start ? gelu_avx512_form(t) : gelu_scalar_form(t);
+        } else {
+            if (ep.gamma) t = mul_rn(t, g[e]);
+            o[e] = EPI == Epi::Residual ? add_rn(x[e], t) : t;
+        }
+    }
+    *c4 = o;
+}
+
+// Split-K reduction fused with the residual update and the LayerNorm of the
+// updated rows: one wave per row (N % 4 == 0, N <= 1024).  Each element is
+// computed exactly as by splitk_reduce_kernel<Residual>, and each row is
+// normalised exactly as by layernorm_kernel, in one pass over the row.  All
+// reads of a lane are issued before any arithmetic (chunks past the row end
+// read chunk 0 and are dropped), so they are in flight together.
+template <int SPLITS>
+__global__ __launch_bounds__(256) void splitk_residual_ln_kernel(int M, int N, EpiArgs ep,
+                                                                 const float *__restrict__ ln_g,
+                                                                 const float *__restrict__ ln_b,
+                                                                 float *__restrict__ ln_out,
+                                                                 float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int n4 = N >> 2;
+    const size_t mn4 = (size_t)M * n4;
+    const f32x4 *part = reinterpret_cast<const f32x4 *>(ep.partial);
+    f32x4 *c4 = reinterpret_cast<f32x4 *>(ep.c + (size_t)row * N);
+    const f32x4 *bias4 = reinterpret_cast<const f32x4 *>(ep.bias);
+    const f32x4 *gamma4 = reinterpret_cast<const f32x4 *>(ep.gamma);
+    f32x4 p[4][SPLITS], x[4], b[4], g[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int idx = lane + j * 64 < n4 ? lane + j * 64 : 0;
+        const size_t i4 = (size_t)row * n4 + idx;
+#pragma unroll
+        for (int sp = 0; sp < SPLITS; sp++) p[j][sp] = part[(size_t)sp * mn4 + i4];
+        x[j] = c4[idx];
+        b[j] = ep.bias ? bias4[idx] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        g[j] = ep.gamma ? gamma4[idx] : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+    }
+    f32x4 r[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const bool live = lane + j * 64 < n4;
+        f32x4 v = p[j][0];
+#pragma unroll
+        for (int sp = 1; sp < SPLITS; sp++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = add_rn(v[e], p[j][sp][e]);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            if (ep.bias) v[e] = add_rn(v[e], b[j][e]);
+            if (ep.gamma) v[e] = mul_rn(v[e], g[j][e]);
+            x[j][e] = add_rn(x[j][e], v[e]);
+        }
+        r[j] = live ? x[j] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (live) c4[lane + j * 64] = x[j];
+    }
+    float mean, inv;
+    ln_row_stats(r, lane, n4, N, eps, mean, inv);
+    f32x4 *y4 = reinterpret_cast<f32x4 *>(ln_out + (size_t)row * N);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int idx = lane + j * 64;
+        if (idx < n4)
+            y4[idx] = ln_apply(r[j], mean, inv, reinterpret_cast<const f32x4 *>(ln_g)[idx],
+                               reinterpret_cast<const f32x4 *>(ln_b)[idx]);
+    }
+}
+
 struct Tile {
     int bm, bn, bk, wm, wn;
 };
@@ -500,6 +599,14 @@ hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
         hipError_t e = run_cfg<EPI, true>(s, g, ep, t, splits);
         if (e != hipSuccess) return e;
         size_t mn = g.m * g.n;
+        if (g.n % 4 == 0 && splits >= 2 && splits <= 4) {
+            const unsigned blocks = (unsigned)((mn / 4 + 255) / 256);
+            const int m = (int)g.m, n = (int)g.n;
+            if (splits == 2) splitk_reduce4_kernel<EPI, 2><<<blocks, 256, 0, s>>>(m, n, ep);
+            else if (splits == 3) splitk_reduce4_kernel<EPI, 3><<<blocks, 256, 0, s>>>(m, n, ep);
+            else splitk_reduce4_kernel<EPI, 4><<<blocks, 256, 0, s>>>(m, n, ep);
+            return hipGetLastError();
+        }
         unsigned blocks = (unsigned)std::min<size_t>((mn / 4 + 255) / 256, 4096);
         if (blocks == 0) blocks = 1;
         splitk_reduce_kernel<EPI><<<blocks, 256, 0, s>>>(splits, (int)g.m, (int)g.n, ep);
@@ -508,6 +615,43 @@ hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
 }
 
 }  // namespace
+
+// Residual GEMM followed by the LayerNorm of the updated rows: split K and
+// fuse the reduction with the normalisation when the shape allows, else run
+// the GEMM and a separate LayerNorm.
+static hipError_t residual_ln(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
+    Tile t;
+    int splits;
+    if (!tile_override(&t, &splits)) {
+        default_tile(g, &t, &splits);
+        if (splits < 2) {
+            t = Tile{64, 64, 32, 2, 2};
+            splits = 3;
+        }
+    }
+    const bool fused = splits >= 2 && splits <= 4 && g.k >= 64 * (size_t)splits && g.n % 4 == 0 && g.n <= 1024 &&
+                       g.ws != nullptr && g.ws_floats >= (size_t)splits * g.m * g.n;
+    if (!fused) {
+        hipError_t e = dispatch<Epi::Residual>(s, g, ep);
+        if (e != hipSuccess) return e;
+        return launch_layernorm(s, g.c, g.ln_gamma, g.ln_beta, g.ln_out, g.m, g.n, g.ln_eps);
+    }
+    ep.partial = g.ws;
+    hipError_t e = run_cfg<Epi::Residual, true>(s, g, ep, t, splits);
+    if (e == hipErrorInvalidValue) {
+        t = Tile{64, 64, 32, 2, 2};
+        e = run_cfg<Epi::Residual, true>(s, g, ep, t, splits);
+    }
+    if (e != hipSuccess) return e;
+    const dim3 grid((unsigned)((g.m + 3) / 4));
+    const int m = (int)g.m, n = (int)g.n;
+    switch (splits) {
+        case 2: splitk_residual_ln_kernel<2><<<grid, 256, 0, s>>>(m, n, ep, g.ln_gamma, g.ln_beta, g.ln_out, g.ln_eps); break;
+        case 3: splitk_residual_ln_kernel<3><<<grid, 256, 0, s>>>(m, n, ep, g.ln_gamma, g.ln_beta, g.ln_out, g.ln_eps); break;
+        default: splitk_residual_ln_kernel<4><<<grid, 256, 0, s>>>(m, n, ep, g.ln_gamma, g.ln_beta, g.ln_out, g.ln_eps); break;
+    }
+    return hipGetLastError();
+}
 
 hipError_t launch_gemm(hipStream_t s, const GemmArgs &g) {
     if (g.m == 0 || g.n == 0) return hipSuccess;
@@ -526,7 +670,8 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs &g) {
     switch (g.epi) {
         case Epi::Store: return dispatch<Epi::Store>(s, g, ep);
         case Epi::Gelu: return dispatch<Epi::Gelu>(s, g, ep);
-        case Epi::Residual: return dispatch<Epi::Residual>(s, g, ep);
+        case Epi::Residual:
+            return g.ln_out ? residual_ln(s, g, ep) : dispatch<Epi::Residual>(s, g, ep);
         case Epi::Qkv: return dispatch<Epi::Qkv>(s, g, ep);
     }
     return hipErrorInvalidValue;

@@ -51,9 +51,13 @@ hipError_t launch_attention_online(hipStream_t s, const float *q, const float *k
                                    size_t head_dim, float scale);
 // fp32-MFMA flash attention, head_dim 64, scale 1/8.  q/k/v [bh][tokens][64]
 // with bh = images*heads; out head-major or token-major [img][tokens][heads*64].
+// Key splits across workgroups need a workspace of flash_workspace_floats()
+// floats; with ws == nullptr (or too small) the kernel runs unsplit.
+constexpr int kMaxFlashSplits = 4;
+size_t flash_workspace_floats(size_t bh, size_t tokens);
 hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k, const float *v,
                                   float *out, size_t bh, size_t tokens, size_t heads,
-                                  bool token_major);
+                                  bool token_major, float *ws, size_t ws_floats);
 
 // ---- GEMM (k_gemm.hip) ----------------------------------------------------
 enum class Epi : int { Store = 0, Gelu = 1, Residual = 2, Qkv = 3 };
@@ -73,6 +77,11 @@ struct GemmArgs {
     // split-K workspace (>= splits * m * n floats) or null (no split)
     float *ws;
     size_t ws_floats;
+    // Residual only: also write LayerNorm(c) row by row to ln_out (the next
+    // sub-layer's input), fused into the split-K reduction when possible.
+    const float *ln_gamma = nullptr, *ln_beta = nullptr;
+    float *ln_out = nullptr;
+    float ln_eps = 0.0f;
 };
 hipError_t launch_gemm(hipStream_t s, const GemmArgs &g);
 

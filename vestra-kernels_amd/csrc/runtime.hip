@@ -84,6 +84,8 @@ struct RtState {
     size_t ws_floats = 0;
     float *sk = nullptr;                        // grow-only split-K partials
     size_t sk_floats = 0;
+    float *fw = nullptr;                        // grow-only attention key-split partials
+    size_t fw_floats = 0;
 
     bool profile = false;
     std::vector<ProfileRec> pending;
@@ -97,6 +99,7 @@ struct RtState {
         for (auto &kv : rope_cache) hipFree(kv.second);
         if (ws) hipFree(ws);
         if (sk) hipFree(sk);
+        if (fw) hipFree(fw);
 
         for (auto &p : pending) {
             hipEventDestroy(p.a);
@@ -331,8 +334,19 @@ vh_status splitk_workspace(RtState &s, size_t m, size_t n, float **out, size_t *
 
 vh_status flash(RtState &s, const float *q, const float *k, const float *v, float *out,
                 size_t bh, size_t tokens, size_t heads, bool token_major) {
+    // Partials of the key splits; without them the kernel runs unsplit.
+    const size_t need = vh::flash_workspace_floats(bh, tokens);
+    if (s.fw_floats < need) {
+        hipStreamSynchronize(s.stream);
+        if (s.fw) hipFree(s.fw);
+        s.fw = nullptr;
+        s.fw_floats = 0;
+        if (hipMalloc(&s.fw, need * sizeof(float)) == hipSuccess) s.fw_floats = need;
+        else hipGetLastError();
+    }
     return launch(s, "flash_attention", [&] {
-        return vh::launch_flash_attention(s.stream, q, k, v, out, bh, tokens, heads, token_major);
+        return vh::launch_flash_attention(s.stream, q, k, v, out, bh, tokens, heads, token_major,
+                                          s.fw, s.fw_floats);
     });
 }
 
@@ -358,8 +372,15 @@ vh_status prepare_lin(RtState &s, size_t K, size_t N, const float *w, const floa
     return VH_OK;
 }
 
+// LayerNorm applied to the rows a Residual GEMM has just updated.
+struct RowNorm {
+    const float *gamma, *beta;
+    float *out;
+    float eps;
+};
+
 vh_status run_lin(RtState &s, const Lin &L, const float *in, size_t rows, vh::Epi epi, float *c,
-                  const char *name) {
+                  const char *name, const RowNorm *norm = nullptr) {
     vh::GemmArgs g{};
     g.a = in;
     g.bt = L.wt;
@@ -370,6 +391,12 @@ vh_status run_lin(RtState &s, const Lin &L, const float *in, size_t rows, vh::Ep
     g.c = c;
     g.bias = L.bias;
     g.gamma = epi == vh::Epi::Gelu ? nullptr : L.gamma;
+    if (norm) {
+        g.ln_gamma = norm->gamma;
+        g.ln_beta = norm->beta;
+        g.ln_out = norm->out;
+        g.ln_eps = norm->eps;
+    }
     TRY(splitk_workspace(s, rows, L.N, &g.ws, &g.ws_floats));
     return launch(s, name, [&] { return vh::launch_gemm(s.stream, g); });
 }
@@ -1400,8 +1427,13 @@ vh_status upload_small(RtState &s, const float *h, size_t n, float **out, const 
     return upload_array(s, h, n, out, what);
 }
 
+// One pre-norm block, in place on x.  With h_ready the caller has already
+// written LayerNorm1(x) into the block workspace (the previous block's fc2
+// fused it); with next, this block's fc2 writes the next block's
+// LayerNorm1(x) there the same way.
 vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size_t tokens,
-                    const int64_t *pos, float freq, float eps) {
+                    const int64_t *pos, float freq, float eps, bool h_ready = false,
+                    const vh_block *next = nullptr) {
     const size_t M = images * tokens;
     const size_t D = kDim;
     float *ws = nullptr;
@@ -1410,18 +1442,20 @@ vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size
           *f = att + M * D;
     const float *rot = nullptr;
     if (pos) TRY(rope_table(s, pos, tokens, 64, freq, &rot));
-    TRY(launch(s, "layernorm", [&] {
-        return vh::launch_layernorm(s.stream, x, b.ln1_g, b.ln1_b, h, M, D, eps);
-    }));
+    if (!h_ready)
+        TRY(launch(s, "layernorm", [&] {
+            return vh::launch_layernorm(s.stream, x, b.ln1_g, b.ln1_b, h, M, D, eps);
+        }));
     TRY(run_qkv(s, b.qkv, h, images, tokens, kHeads, rot, q, k, v));
     TRY(flash(s, q, k, v, att, images * kHeads, tokens, kHeads, true));
-    TRY(run_lin(s, b.proj, att, M, vh::Epi::Residual, x, "gemm_proj_residual"));
-    TRY(launch(s, "layernorm", [&] {
-        return vh::launch_layernorm(s.stream, x, b.ln2_g, b.ln2_b, h, M, D, eps);
-    }));
+    const RowNorm ln2{b.ln2_g, b.ln2_b, h, eps};
+    TRY(run_lin(s, b.proj, att, M, vh::Epi::Residual, x, "gemm_proj_residual_ln", &ln2));
     TRY(run_lin(s, b.fc1, h, M, vh::Epi::Gelu, f, "gemm_fc1_gelu"));
-    TRY(run_lin(s, b.fc2, f, M, vh::Epi::Residual, x, "gemm_fc2_residual"));
-    return VH_OK;
+    if (next) {
+        const RowNorm ln1{next->ln1_g, next->ln1_b, h, eps};
+        return run_lin(s, b.fc2, f, M, vh::Epi::Residual, x, "gemm_fc2_residual_ln", &ln1);
+    }
+    return run_lin(s, b.fc2, f, M, vh::Epi::Residual, x, "gemm_fc2_residual");
 }
 
 vh_status check_block_x(const vh_tensor *x, size_t images, size_t tokens) {
@@ -1497,7 +1531,8 @@ extern "C" vh_status vh_encoder_run(const vh_runtime *rt, const vh_block *const 
     TRY(set_device(s));
     if (images * tokens == 0) return VH_OK;
     for (size_t i = 0; i < layers; i++)
-        TRY(block_run(s, *blocks[i], x->ptr, images, tokens, pos_yx, rope_frequency, epsilon));
+        TRY(block_run(s, *blocks[i], x->ptr, images, tokens, pos_yx, rope_frequency, epsilon,
+                      i > 0, i + 1 < layers ? blocks[i + 1] : nullptr));
     return VH_OK;
     GUARD_END
 }
