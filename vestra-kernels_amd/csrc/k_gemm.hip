@@ -54,6 +54,39 @@ __device__ __forceinline__ void epilogue_store(const EpiArgs &ep, size_t idx, in
     }
 }
 
+// Workgroup -> (row tile, column tile, split).  The hardware deals
+// workgroups round-robin over the 8 XCDs, each with its own L2; the linear
+// id is renumbered so that each XCD receives a contiguous run of tile ids
+// (a bijection: the first total % 8 XCDs take one more), and tile ids walk
+// groups of 8 row tiles column by column, so the run of one XCD covers a
+// compact block of C and fetches fewer A row panels and B column panels.
+// Measured on MI355X this pays for the batched shapes (M = 4 x 865) and costs
+// a little at M = 865, where the GEMMs are not fetch-bound; without
+// xcd_order the tiles follow the launch grid.
+__device__ __forceinline__ void tile_of_block(bool xcd_order, int &tm, int &tn, int &z) {
+    if (!xcd_order) {
+        tm = blockIdx.y;
+        tn = blockIdx.x;
+        z = blockIdx.z;
+        return;
+    }
+    const int nx = gridDim.x, ny = gridDim.y;
+    const int total = nx * ny * gridDim.z;
+    const int bid = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+    const int q = total / 8, r = total % 8, x = bid % 8;
+    const int pid = x * q + min(x, r) + bid / 8;
+    const int per = nx * ny;
+    z = pid / per;
+    const int t = pid - z * per;
+    const int gm = min(8, ny);
+    const int group = t / (gm * nx);
+    const int first = group * gm;
+    const int rows = min(ny - first, gm);
+    const int local = t - group * gm * nx;
+    tm = first + local % rows;
+    tn = local / rows;
+}
+
 // EXACT: K and the split length are multiples of BK and K % 4 == 0, so every
 // k-slice is whole.  Rows past M (columns past N) load a clamped in-range row
 // and are NOT zeroed: C[m][n] depends only on A row m and Bt row n, and rows
@@ -64,7 +97,8 @@ template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXAC
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__restrict__ A,
                                                               const float *__restrict__ Bt,
                                                               int M, int N, int K,
-                                                              int k_per_split, EpiArgs ep) {
+                                                              int k_per_split, int xcd_order,
+                                                              EpiArgs ep) {
     constexpr int NT = WM * WN * 64;
     constexpr int LDK = BK + 4;
     constexpr int CPR = BK / 4;  // float4 chunks per row slice
@@ -85,8 +119,10 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lh = lane >> 4;
     const int wm = wave / WN, wn = wave % WN;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int kbeg = blockIdx.z * k_per_split;
+    int tile_m, tile_n, split;
+    tile_of_block(xcd_order != 0, tile_m, tile_n, split);
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    const int kbeg = split * k_per_split;
     const int kend = min(K, kbeg + k_per_split);
     const bool vec = (K & 3) == 0;
 
@@ -236,7 +272,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     // C fragment layout: register r of lane l holds row 4*(l/16)+r, column l%16.
     const int rbase = m0 + wm * TM + 4 * lh;
     if constexpr (SPLIT) {
-        float *part = ep.partial + (size_t)blockIdx.z * M * N;
+        float *part = ep.partial + (size_t)split * M * N;
         const int cbase = n0 + wn * TN + li;
 #pragma unroll
         for (int j = 0; j < FN; j++) {
@@ -500,7 +536,8 @@ hipError_t launch_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int 
         configured = true;
     }
     dim3 grid((unsigned)((g.n + BN - 1) / BN), (unsigned)((g.m + BM - 1) / BM), (unsigned)splits);
-    kernel<<<grid, WM * WN * 64, lds, s>>>(g.a, g.bt, (int)g.m, (int)g.n, (int)g.k, kps, ep);
+    const int xcd_order = g.m > 1024;
+    kernel<<<grid, WM * WN * 64, lds, s>>>(g.a, g.bt, (int)g.m, (int)g.n, (int)g.k, kps, xcd_order, ep);
     return hipGetLastError();
 }
 
