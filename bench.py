@@ -46,6 +46,24 @@ FLOPS = {
 BYTES = {"layernorm": 2.0 * T * D * 4 + 2 * D * 4}
 
 
+TRAFFIC_SUMMARY = ROOT / "profiles" / "block_865_hbm_traffic.md"
+
+
+def measured_traffic(launch: str):
+    """HBM bytes per launch of `launch` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel), or
+    None when the summary has no row for it."""
+    try:
+        text = TRAFFIC_SUMMARY.read_text()
+    except OSError:
+        return None
+    for line in text.splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 5 and cells[0] == f"`{launch}`" and cells[2].isdigit():
+            return int(cells[2])
+    return None
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -179,7 +197,8 @@ def main() -> int:
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",
             "frac": d["frac_fp32_mfma"],
-            "traffic": None,
+            "traffic": measured_traffic(dominant),
+            "traffic_unit": "bytes per launch (profiles/block_865_hbm_traffic.md)",
         },
         "kernels": ker,
     }
