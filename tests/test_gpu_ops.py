@@ -351,10 +351,12 @@ def test_quantize_q8_0_bit_exact(rt, rows, k):
     assert np.array_equal(got["qs"], exp["qs"])
 
 
-@pytest.mark.parametrize("m,n,k", [(865, 3072, 768), (8, 8, 64), (5, 17, 96)])
+@pytest.mark.parametrize("m,n,k", [(865, 3072, 768), (8, 8, 64), (5, 17, 96), (64, 96, 3072),
+                                   (33, 70, 1056)])
 def test_gemm_q8_0_bit_exact(rt, m, n, k):
     """BASELINE config 4 (fc1 weights N(0, 0.02^2), activations N(0,1) quantised
-    on the device) and the tests/q8_0_dot_matches_f32.rs shape."""
+    on the device), the tests/q8_0_dot_matches_f32.rs shape, and K spanning
+    several 32-block scale chunks (3072) or ending in a one-block chunk (1056)."""
     x = seeded.normal(91, m * k)
     w = seeded.normal(92, k * n, 0.02)
     wt = np.ascontiguousarray(w.reshape(k, n).T).reshape(-1)

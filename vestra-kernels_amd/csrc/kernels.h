@@ -86,7 +86,7 @@ struct GemmArgs {
 hipError_t launch_gemm(hipStream_t s, const GemmArgs &g);
 
 // ---- Q8_0 (k_q8.hip) --------------------------------------------------------
-// x [rows][k] -> qs [rows][k] int8, d [rows][k/32] f16 bits
+// x [rows][k] -> block-major Q8_0: qs [k/32][rows][32] int8, d [k/32][rows] f16 bits
 hipError_t launch_quantize_q8_0(hipStream_t s, const float *x, int8_t *qs, uint16_t *d,
                                 size_t rows, size_t k);
 hipError_t launch_gemm_q8_0(hipStream_t s, const int8_t *a_qs, const uint16_t *a_d,

@@ -1300,15 +1300,17 @@ extern "C" vh_status vh_q8_0_upload(const vh_runtime *rt, const void *blocks, si
     GUARD_BEGIN
     RtState &s = *rt->s;
     TRY(set_device(s));
-    const size_t nb = n / 32;
+    // AoS block (row r, k-slice j) -> block-major slot j * rows + r.
+    const size_t nb = n / 32, nbr = k / 32;
     std::vector<int8_t> qs(n);
     std::vector<uint16_t> d(nb);
     const BlockQ8 *src = static_cast<const BlockQ8 *>(blocks);
     for (size_t b = 0; b < nb; b++) {
         BlockQ8 blk;
         std::memcpy(&blk, src + b, sizeof(blk));
-        d[b] = blk.d;
-        std::memcpy(&qs[b * 32], blk.qs, 32);
+        const size_t slot = (b % nbr) * rows + b / nbr;
+        d[slot] = blk.d;
+        std::memcpy(&qs[slot * 32], blk.qs, 32);
     }
     vh_q8_tensor *t = nullptr;
     TRY(new_q8(rt->s, rows, k, &t));
@@ -1344,10 +1346,12 @@ extern "C" vh_status vh_q8_0_download(const vh_runtime *rt, const vh_q8_tensor *
     }
     if (e != hipSuccess) return fail(VH_ERR_DOWNLOAD, hip_msg("Q8_0 download", e));
     BlockQ8 *dst = static_cast<BlockQ8 *>(blocks);
+    const size_t nbr = tensor->k / 32;
     for (size_t b = 0; b < nb; b++) {
+        const size_t slot = (b % nbr) * tensor->rows + b / nbr;
         BlockQ8 blk;
-        blk.d = d[b];
-        std::memcpy(blk.qs, &qs[b * 32], 32);
+        blk.d = d[slot];
+        std::memcpy(blk.qs, &qs[slot * 32], 32);
         std::memcpy(dst + b, &blk, sizeof(blk));
     }
     return VH_OK;
