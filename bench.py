@@ -111,6 +111,43 @@ def gpu_block(steps: int, warmup: int) -> dict:
     return {"ms_per_step": total_ms / steps, "kernels": kernels}
 
 
+def gpu_q8_0(steps: int) -> dict:
+    """fc1-shaped Q8_0 path.  X [865, 768] ~ N(0,1)
+    quantised on the device each step, W [768, 3072] ~ N(0, 0.02^2)
+    quantised along K at load time, C = X_q . W_q [865, 3072] f32."""
+    import vestra_hip as vh
+    from vestra_hip import seeded
+
+    rt = vh.Runtime(0)
+    m, k, n = T, D, F
+    x = rt.upload_f32(seeded.normal(11, m * k))
+    w = seeded.normal(12, k * n, 0.02).reshape(k, n)
+    wq = rt.quantize_q8_0(rt.upload_f32(np.ascontiguousarray(w.T).reshape(-1)), n, k)
+    for _ in range(3):
+        rt.gemm_q8_0(rt.quantize_q8_0(x, m, k), wq, m, n, k)
+    rt.synchronize()
+    rt.profile_reset()
+    rt.profile_enable(True)
+    keep = []  # outputs stay alive: no stream-ordered frees between the timed launches
+    for _ in range(steps):
+        aq = rt.quantize_q8_0(x, m, k)
+        keep.append((aq, rt.gemm_q8_0(aq, wq, m, n, k)))
+    prof = rt.profile_report()
+    rt.profile_enable(False)
+    del keep
+    q_us = 1e3 * prof["quantize_q8_0"][1] / prof["quantize_q8_0"][0]
+    g_us = 1e3 * prof["gemm_q8_0"][1] / prof["gemm_q8_0"][0]
+    gemm_bytes = m * k + m * (k // 32) * 2 + n * k + n * (k // 32) * 2 + m * n * 4
+    quant_bytes = m * k * 4 + m * k + m * (k // 32) * 2
+    gbs = gemm_bytes / (g_us * 1e-6) / 1e9
+    log(f"  q8_0 quantize {q_us:.2f} us, gemm {g_us:.2f} us ({gbs:.0f} GB/s algorithmic)")
+    return {"workload": "q8_0_fc1_865", "quantize_us": round(q_us, 3), "gemm_us": round(g_us, 3),
+            "gemm_top_s": round(2.0 * m * n * k / (g_us * 1e-6) / 1e12, 1),
+            "gemm_algorithmic_bytes": gemm_bytes, "gemm_gbs": round(gbs, 1),
+            "gemm_frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "quantize_algorithmic_bytes": quant_bytes,
+            "quantize_gbs": round(quant_bytes / (q_us * 1e-6) / 1e9, 1)}
+
+
 def cpu_block(budget_s: float) -> dict:
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
@@ -157,6 +194,7 @@ def main() -> int:
         return 2
 
     gpu = gpu_block(args.steps, args.warmup)
+    q8 = gpu_q8_0(max(10, min(args.steps, 100)))
     if args.calibrate:
         import vestra_hip as vh
 
@@ -201,6 +239,7 @@ def main() -> int:
             "traffic_unit": "bytes per launch (profiles/block_865_hbm_traffic.md)",
         },
         "kernels": ker,
+        "q8_0": q8,
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_block(args.cpu_seconds)
