@@ -312,6 +312,297 @@ __global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2)
         *reinterpret_cast<f32x4 *>(orow + 16 * df + 4 * lh) = o[df] * inv;
 }
 
+// Software-pipelined form for one key stream per workgroup: while the
+// MFMAs of S(j+1) = K(j+1) . Q^T run, the same wave's VALU computes the
+// online softmax of panel j, so MFMA and softmax no longer alternate.  LDS
+// stage j holds K(j+1) and V(j) (keys lead values by one panel): iteration j
+// reads stage j and fills stage j+1 with K(j+2), V(j+1), in the buffer that
+// last held stage j-1, read before the previous barrier.  The last panel is
+// peeled so no MFMA work goes to a panel that does not exist.  Two
+// workgroups share a CU (two waves per SIMD), so a wave has 256 registers.
+template <bool TOKEN_MAJOR, bool SPLIT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void flash_pipe_kernel(
+    FlashArgs fa) {
+    constexpr int NT = 256;
+    constexpr int KSTAGE = BKV * LDP;  // floats of one K stage
+    constexpr int VSTAGE = D * BKV;    // floats of one V^T stage
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float *Ks = smem;               // [2][BKV*LDP]
+    float *Vs = smem + 2 * KSTAGE;  // [2][D*BKV], transposed and swizzled
+
+    const int splits = SPLIT ? fa.splits : 1;
+    const int total = fa.bh * fa.qtiles * splits;
+    int item = blockIdx.x;
+    if (fa.xcd_map) {
+        const int per_xcd = (total + 7) / 8;
+        item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+        if (item >= total) return;
+    }
+    const int z = item % splits;
+    const int qt = (item / splits) % fa.qtiles;
+    const int bh = item / splits / fa.qtiles;
+    const int T = fa.T;
+    const int kb = SPLIT ? z * fa.split_keys : 0;
+    const int ke = SPLIT ? min(T, kb + fa.split_keys) : T;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lh = lane >> 4;
+    const size_t head_off = (size_t)bh * T * D;
+    const float *Qh = fa.q + head_off;
+    const float *Kh = fa.k + head_off;
+    const float *Vh = fa.v + head_off;
+    const int query = qt * BQ + wave * 16 + li;
+    f32x4 qf[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        qf[c] = query < T ? *reinterpret_cast<const f32x4 *>(Qh + (size_t)query * D + 16 * c + 4 * lh)
+                          : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    constexpr int CH = BKV * 16 / NT;  // float4 chunks per thread and panel (= 4)
+    f32x4 rk[CH], rv[CH];
+    auto gload_k = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
+            rk[i] = *reinterpret_cast<const f32x4 *>(Kh + (size_t)min(k0 + key, ke - 1) * D + d4);
+        }
+    };
+    auto gload_v = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
+            rv[i] = *reinterpret_cast<const f32x4 *>(Vh + (size_t)min(k0 + key, ke - 1) * D + d4);
+        }
+    };
+    auto store_k = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
+            *reinterpret_cast<f32x4 *>(&Ks[buf * KSTAGE + key * LDP + d4]) = rk[i];
+        }
+    };
+    auto store_v = [&](int buf, int k0) {
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
+            const unsigned keep = k0 + key < ke ? 0xffffffffu : 0u;  // keys past ke: +0 rows
+            float *vt = Vs + buf * VSTAGE;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int d = d4 + e;
+                vt[d * BKV + (key ^ vswz(d))] = __uint_as_float(__float_as_uint(rv[i][e]) & keep);
+            }
+        }
+    };
+    int vcol[4];
+#pragma unroll
+    for (int df = 0; df < 4; df++) vcol[df] = vswz(16 * df + li);
+    f32x4 kf[4][4], vf[4][4];
+    auto read_kf = [&](int buf) {
+        const float *ks = Ks + buf * KSTAGE + li * LDP + 4 * lh;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                kf[g][c] = *reinterpret_cast<const f32x4 *>(&ks[16 * g * LDP + 16 * c]);
+    };
+    auto read_vf = [&](int buf) {
+        const float *vt = Vs + buf * VSTAGE;
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int df = 0; df < 4; df++)
+                vf[g][df] = *reinterpret_cast<const f32x4 *>(
+                    &vt[(16 * df + li) * BKV + ((16 * g + 4 * lh) ^ vcol[df])]);
+    };
+    // S^T fragments: s[g][r] = S[key 16g+4lh+r][query li].
+    auto qk = [&](f32x4 (&sc)[4]) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) sc[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int st = 0; st < 4; st++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) sc[g] = mfma16x16x4(kf[g][c][st], qf[c][st], sc[g]);
+    };
+    const float scale = 0.125f * kLog2e;
+    float m = -INFINITY, l = 0.0f;
+    f32x4 o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // Online softmax of panel k0 in place (scores -> probabilities).
+    auto softmax = [&](f32x4 (&sc)[4], int k0) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int key = k0 + 16 * g + 4 * lh + r;
+                const float t = key < ke ? sc[g][r] * scale : -INFINITY;
+                sc[g][r] = t;
+                mx = fmaxf(mx, t);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(m, mx);
+        const float mref = mnew == -INFINITY ? 0.0f : mnew;
+        const float corr = __builtin_amdgcn_exp2f(m - mref);
+        float psum = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float pv = __builtin_amdgcn_exp2f(sc[g][r] - mref);
+                sc[g][r] = pv;
+                psum += pv;
+            }
+        l = l * corr + psum;
+        m = mnew;
+#pragma unroll
+        for (int df = 0; df < 4; df++) o[df] *= corr;
+    };
+    // O^T[d][query] += V^T[d][key] P^T[key][query].
+    auto pv = [&](const f32x4 (&pr)[4]) {
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int st = 0; st < 4; st++)
+#pragma unroll
+                for (int df = 0; df < 4; df++) o[df] = mfma16x16x4(vf[g][df][st], pr[g][st], o[df]);
+    };
+
+    const int n = (ke - kb + BKV - 1) / BKV;  // panels of this workgroup, >= 1
+    auto pk = [&](int j) { return kb + min(j, n - 1) * BKV; };
+
+    // Prologue: K(0) into buffer 1, S(0); stage 0 = K(1), V(0) into buffer 0.
+    gload_k(pk(0));
+    store_k(1);
+    gload_k(pk(1));
+    gload_v(pk(0));
+    __syncthreads();
+    f32x4 s_cur[4], s_next[4];
+    read_kf(1);
+    qk(s_cur);
+    store_k(0);
+    store_v(0, pk(0));
+    __syncthreads();
+
+    for (int j = 0; j + 1 < n; j++) {
+        const int buf = j & 1;
+        // QK phase: K(j+2) is fetched, K(j+1) is read, and the QK MFMAs of
+        // panel j+1 run with the softmax VALU work of panel j between them.
+        gload_k(pk(j + 2));
+        read_kf(buf);
+        __builtin_amdgcn_sched_barrier(0);
+        // The 64 QK MFMAs go out in 16 steps of four (one (c, st) k-slice for
+        // the four key groups); after each step comes one sixteenth of the
+        // softmax of panel j, fenced so that the compiler keeps the order.
+        {
+            const int k0 = kb + j * BKV;
+            float mxg[4], mx = 0.0f, sh = 0.0f, mnew = 0.0f, mref = 0.0f, corr = 0.0f, psum = 0.0f;
+#pragma unroll
+            for (int g = 0; g < 4; g++) s_next[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int step = 0; step < 16; step++) {
+                const int c = step >> 2, st = step & 3;
+#pragma unroll
+                for (int g = 0; g < 4; g++) s_next[g] = mfma16x16x4(kf[g][c][st], qf[c][st], s_next[g]);
+                if (step < 4) {  // scale and mask key group g = step
+                    const int g = step;
+                    float mg = -INFINITY;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int key = k0 + 16 * g + 4 * lh + r;
+                        const float t = key < ke ? s_cur[g][r] * scale : -INFINITY;
+                        s_cur[g][r] = t;
+                        mg = fmaxf(mg, t);
+                    }
+                    mxg[g] = mg;
+                } else if (step == 4) {  // each shuffle is used one step after its issue
+                    mx = fmaxf(fmaxf(mxg[0], mxg[1]), fmaxf(mxg[2], mxg[3]));
+                    sh = __shfl_xor(mx, 16, 64);
+                } else if (step == 5) {
+                    mx = fmaxf(mx, sh);
+                    sh = __shfl_xor(mx, 32, 64);
+                } else if (step == 6) {
+                    mx = fmaxf(mx, sh);
+                    mnew = fmaxf(m, mx);
+                    // A key range with no valid key yet keeps m = -inf; 0 as
+                    // the reference makes exp2 see -inf (giving 0), never NaN.
+                    mref = mnew == -INFINITY ? 0.0f : mnew;
+                    corr = __builtin_amdgcn_exp2f(m - mref);
+                } else if (step < 11) {  // probabilities of key group g
+                    const int g = step - 7;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float pv = __builtin_amdgcn_exp2f(s_cur[g][r] - mref);
+                        s_cur[g][r] = pv;
+                        psum += pv;
+                    }
+                } else if (step == 11) {
+                    l = l * corr + psum;
+                    m = mnew;
+                } else {  // rescale output fragment df
+                    o[step - 12] *= corr;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // PV phase: V(j+1) is fetched; the V fragments of key group g+1 are
+        // read during the MFMAs of group g, so only one fragment set is live
+        // at a time; K(j+2) and V(j+1) are stored into the other buffer (it
+        // last held stage j-1, read before the previous barrier).
+        gload_v(pk(j + 1));
+        read_vf(buf);
+        pv(s_cur);
+        store_k(buf ^ 1);
+        store_v(buf ^ 1, pk(j + 1));
+        __builtin_amdgcn_sched_group_barrier(0x020, CH, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 12; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 5 * CH - 4; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < 4; g++) s_cur[g] = s_next[g];
+    }
+    read_vf((n - 1) & 1);
+    softmax(s_cur, kb + (n - 1) * BKV);
+    pv(s_cur);
+
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (query >= T) return;
+    if constexpr (SPLIT) {
+        const size_t prow = ((size_t)z * fa.bh + bh) * T + query;
+        float *orow = fa.po + prow * D;
+#pragma unroll
+        for (int df = 0; df < 4; df++) *reinterpret_cast<f32x4 *>(orow + 16 * df + 4 * lh) = o[df];
+        if (lh == 0) fa.pml[prow] = make_float2(m, l);
+        return;
+    }
+    const float inv = 1.0f / l;
+    float *orow;
+    if constexpr (TOKEN_MAJOR) {
+        const int img = bh / fa.heads, head = bh % fa.heads;
+        orow = fa.out + ((size_t)img * T + query) * ((size_t)fa.heads * D) + (size_t)head * D;
+    } else {
+        orow = fa.out + head_off + (size_t)query * D;
+    }
+#pragma unroll
+    for (int df = 0; df < 4; df++) *reinterpret_cast<f32x4 *>(orow + 16 * df + 4 * lh) = o[df] * inv;
+}
+
 // Combines the key splits of each (head, query) in split order:
 // O = sum_z 2^(m_z - M) o_z / sum_z 2^(m_z - M) l_z with M = max_z m_z.
 // One thread per four output dims; all reads are issued first.
@@ -373,6 +664,30 @@ hipError_t run_flash(hipStream_t s, const FlashArgs &fa) {
         if (fa.splits == 2) flash_merge_kernel<TOKEN_MAJOR, 2><<<grid, 256, 0, s>>>(fa);
         else if (fa.splits == 3) flash_merge_kernel<TOKEN_MAJOR, 3><<<grid, 256, 0, s>>>(fa);
         else flash_merge_kernel<TOKEN_MAJOR, 4><<<grid, 256, 0, s>>>(fa);
+    }
+    return hipGetLastError();
+}
+
+template <bool TOKEN_MAJOR, bool SPLIT>
+hipError_t run_flash_pipe(hipStream_t s, const FlashArgs &fa) {
+    constexpr size_t lds = 2 * (size_t)(BKV * LDP + D * BKV) * sizeof(float);
+    auto kernel = flash_pipe_kernel<TOKEN_MAJOR, SPLIT>;
+    static bool configured = false;
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    const int total = fa.bh * fa.qtiles * (SPLIT ? fa.splits : 1);
+    const int grid = fa.xcd_map ? (total + 7) / 8 * 8 : total;
+    kernel<<<grid, 256, lds, s>>>(fa);
+    if constexpr (SPLIT) {
+        const size_t threads = (size_t)fa.bh * fa.T * 16;
+        const dim3 mgrid((unsigned)((threads + 255) / 256));
+        if (fa.splits == 2) flash_merge_kernel<TOKEN_MAJOR, 2><<<mgrid, 256, 0, s>>>(fa);
+        else if (fa.splits == 3) flash_merge_kernel<TOKEN_MAJOR, 3><<<mgrid, 256, 0, s>>>(fa);
+        else flash_merge_kernel<TOKEN_MAJOR, 4><<<mgrid, 256, 0, s>>>(fa);
     }
     return hipGetLastError();
 }
@@ -477,17 +792,23 @@ hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k,
     if (const char *e = std::getenv("VESTRA_HIP_FLASH_STREAMS"))
         if (splits == 1) streams = std::atoi(e) == 2 ? 2 : 1;
 
+    // One-stream layouts run the software-pipelined kernel
+    // (VESTRA_HIP_FLASH_PIPE=0 selects the plain loop for A/B runs).
+    bool pipe = true;
+    if (const char *e = std::getenv("VESTRA_HIP_FLASH_PIPE")) pipe = std::atoi(e) != 0;
     if (splits > 1) {
         fa.splits = splits;
         fa.split_keys = split_keys(splits);
         fa.po = ws;
         fa.pml = reinterpret_cast<float2 *>(ws + (size_t)splits * bh * tokens * D);
+        if (pipe) return token_major ? run_flash_pipe<true, true>(s, fa) : run_flash_pipe<false, true>(s, fa);
         return token_major ? run_flash<true, 1, true>(s, fa) : run_flash<false, 1, true>(s, fa);
     }
     fa.splits = 1;
     fa.split_keys = (int)tokens;
     if (streams == 2)
         return token_major ? run_flash<true, 2, false>(s, fa) : run_flash<false, 2, false>(s, fa);
+    if (pipe) return token_major ? run_flash_pipe<true, false>(s, fa) : run_flash_pipe<false, false>(s, fa);
     return token_major ? run_flash<true, 1, false>(s, fa) : run_flash<false, 1, false>(s, fa);
 }
 
