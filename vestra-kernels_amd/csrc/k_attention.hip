@@ -321,7 +321,7 @@ __global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2)
 // peeled so no MFMA work goes to a panel that does not exist.  Two
 // workgroups share a CU (two waves per SIMD), so a wave has 256 registers.
 template <bool TOKEN_MAJOR, bool SPLIT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void flash_pipe_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_pipe_kernel(
     FlashArgs fa) {
     constexpr int NT = 256;
     constexpr int KSTAGE = BKV * LDP;  // floats of one K stage
@@ -490,9 +490,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 
     for (int j = 0; j + 1 < n; j++) {
         const int buf = j & 1;
-        // QK phase: K(j+2) is fetched, K(j+1) is read, and the QK MFMAs of
-        // panel j+1 run with the softmax VALU work of panel j between them.
+        // QK phase: K(j+2) and V(j+1) are fetched, K(j+1) is read, and the QK
+        // MFMAs of panel j+1 run with the softmax VALU work of panel j
+        // between them.
         gload_k(pk(j + 2));
+        gload_v(pk(j + 1));
         read_kf(buf);
         __builtin_amdgcn_sched_barrier(0);
         // The 64 QK MFMAs go out in 16 steps of four (one (c, st) k-slice for
@@ -549,29 +551,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        // PV phase: V(j+1) is fetched; the V fragments of key group g+1 are
-        // read during the MFMAs of group g, so only one fragment set is live
-        // at a time; K(j+2) and V(j+1) are stored into the other buffer (it
-        // last held stage j-1, read before the previous barrier).
-        gload_v(pk(j + 1));
-        read_vf(buf);
-        pv(s_cur);
+        // Stage j+1 (K(j+2), V(j+1)) goes into the other buffer, which last
+        // held stage j-1, read before the previous barrier; the loads have
+        // had the whole QK phase to arrive.
         store_k(buf ^ 1);
         store_v(buf ^ 1, pk(j + 1));
-        __builtin_amdgcn_sched_group_barrier(0x020, CH, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        // PV phase: the V fragments of key group g+1 are read during the
+        // MFMAs of group g, so only one fragment set is live at a time.
+        read_vf(buf);
+        pv(s_cur);
         __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
         for (int i = 0; i < 12; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
         }
-#pragma unroll
-        for (int i = 0; i < 5 * CH - 4; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
         __syncthreads();
 #pragma unroll
         for (int g = 0; g < 4; g++) s_cur[g] = s_next[g];
