@@ -228,13 +228,19 @@ typedef struct vh_block_params {
     const float *w_fc1, *b_fc1;        /* [768*3072], [3072] */
     const float *w_fc2, *b_fc2;        /* [3072*768], [768] */
     const float *ls2;                  /* [768] */
+    /* DA3 late blocks: LayerNorm of each 64-wide Q and K head row before the
+     * RoPE (qk_norm_rope_f32_da3_base, src/specialized.rs:278-316).  All four
+     * NULL for a plain block, all four [64] otherwise. */
+    const float *q_norm_gamma, *q_norm_beta, *k_norm_gamma, *k_norm_beta;
 } vh_block_params;
 
 /* Uploads and repacks one block's weights (model-load time). */
 vh_status vh_block_prepare(const vh_runtime *rt, const vh_block_params *params, vh_block **out);
 void vh_block_free(vh_block *block);
 /* One pre-LN DA3-BASE block in place on x [images*tokens*768]: LN, QKV (+bias,
- * + 2-D RoPE when pos_yx != NULL), attention, out-proj (+bias, *ls1) +
+ * + 2-D RoPE when pos_yx != NULL; a late block first normalises each Q and K
+ * head row, with all tokens at (0, 0) when pos_yx is NULL), attention,
+ * out-proj (+bias, *ls1) +
  * residual, LN, fc1 (+bias, GELU), fc2 (+bias, *ls2) + residual.  The CPU
  * composition it replaces chains src/scalar.rs:83, src/specialized.rs:996,
  * src/rope.rs:30, src/attention.rs:66, src/specialized.rs:811,

@@ -92,7 +92,12 @@ def _declare(L):
 class BlockWeights(ctypes.Structure):
     _fields_ = [(n, _f32p) for n in (
         "ln1_gamma", "ln1_beta", "w_qkv", "b_qkv", "w_proj", "b_proj", "ls1",
-        "ln2_gamma", "ln2_beta", "w_fc1", "b_fc1", "w_fc2", "b_fc2", "ls2")]
+        "ln2_gamma", "ln2_beta", "w_fc1", "b_fc1", "w_fc2", "b_fc2", "ls2",
+        "q_norm_gamma", "q_norm_beta", "k_norm_gamma", "k_norm_beta")]
+
+
+# DA3 late-block Q/K LayerNorm parameters: optional (absent -> plain block).
+QK_NORM_FIELDS = ["q_norm_gamma", "q_norm_beta", "k_norm_gamma", "k_norm_beta"]
 
 
 def _f(a: np.ndarray):
@@ -364,14 +369,14 @@ def hnd_to_token(hnd, tokens, heads, hd):
 
 
 # ---- block -----------------------------------------------------------------
-BLOCK_FIELDS = [f for f, _ in BlockWeights._fields_]
+BLOCK_FIELDS = [f for f, _ in BlockWeights._fields_ if f not in QK_NORM_FIELDS]
 
 
 def vit_block(x, weights: dict, images, tokens, pos_yx=None, rope_freq=100.0, eps=1e-6,
               taps=False):
     """One DA3-BASE encoder block per image (engine composition of the crate's kernels)."""
     xs = f32(x).copy()
-    keep = {n: f32(weights[n]) for n in BLOCK_FIELDS}
+    keep = {n: f32(weights[n]) for n in BLOCK_FIELDS + QK_NORM_FIELDS if weights.get(n) is not None}
     bw = BlockWeights(**{n: _f(a) for n, a in keep.items()})
     pos = None if pos_yx is None else np.ascontiguousarray(pos_yx, np.int64)
     t_ln = t_att = t_gelu = None

@@ -1161,8 +1161,17 @@ void vko_vit_block(float *x_all, size_t images, size_t tokens, const vko_block_w
         if (tap_ln1) memcpy(tap_ln1 + img * T * D, h, T * D * sizeof(float));
         /* QKV with bias, head-major (src/specialized.rs:996) */
         vko_qkv(T, h, w->w_qkv, w->b_qkv, qb, kb, vb);
-        /* 2-D RoPE on Q and K (src/rope.rs:30) */
-        if (pos_yx) {
+        if (w->q_norm_gamma) {
+            /* late block: Q/K LayerNorm fused with the RoPE
+             * (src/specialized.rs:278-316); without positions every token
+             * sits at (0, 0), whose rotation (sin 0, cos 1) is exact identity */
+            int64_t *zero = NULL;
+            if (!pos_yx) zero = (int64_t *)calloc(T * 2, sizeof(int64_t));
+            vko_qk_norm_rope(qb, kb, H, T, w->q_norm_gamma, w->q_norm_beta, w->k_norm_gamma,
+                             w->k_norm_beta, pos_yx ? pos_yx : zero, rope_freq, eps);
+            free(zero);
+        } else if (pos_yx) {
+            /* 2-D RoPE on Q and K (src/rope.rs:30) */
             vko_rope2d(qb, H, T, 64, pos_yx, rope_freq);
             vko_rope2d(kb, H, T, 64, pos_yx, rope_freq);
         }

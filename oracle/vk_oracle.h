@@ -125,6 +125,10 @@ typedef struct vko_block_weights {
     const float *w_fc1, *b_fc1;         /* [768*3072], [3072] */
     const float *w_fc2, *b_fc2;         /* [3072*768], [768] */
     const float *ls2;                   /* [768] */
+    /* DA3 late blocks: LayerNorm of each 64-wide Q and K head row before the
+     * RoPE (qk_norm_rope_f32_da3_base, src/specialized.rs:278-316); all NULL
+     * for a plain block. */
+    const float *q_norm_gamma, *q_norm_beta, *k_norm_gamma, *k_norm_beta; /* [64] */
 } vko_block_weights;
 
 /* x: [images*tokens*768] token-major, updated in place.  pos_yx: [tokens*2]

@@ -11,6 +11,7 @@ import pytest
 
 import oracle as O
 from conftest import max_rel
+import vestra_hip as vh
 from vestra_hip import da3, seeded
 
 pytestmark = pytest.mark.gpu
@@ -113,3 +114,46 @@ def test_encoder_fused_norms_match_block_by_block_runs(rt, images, T):
     a, b = rt.download_f32(fused), rt.download_f32(step)
     assert np.isfinite(a).all()
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("layout, T", [("local", 865), ("global", 865), ("none", 97)])
+def test_late_block_qk_norm_vs_oracle(rt, layout, T):
+    """DA3 late blocks: each 64-wide Q and K head row is LayerNormed before the
+    RoPE (src/specialized.rs:278-316); the global layout puts every patch at
+    (1, 1) (src/specialized.rs:353-358)."""
+    w = da3.block_weights(seed=21, layerscale=1.0, qk_norm=True)
+    x = seeded.normal(2100 + T, T * 768)
+    pos = {"local": da3.positions_yx(24, 36), "global": da3.positions_global(24, 36),
+           "none": None}[layout]
+    exp = O.vit_block(x, w, 1, T, pos)
+    blk = rt.prepare_block(w)
+    xt = rt.upload_f32(x)
+    rt.vit_block_run(blk, xt, 1, T, pos)
+    got = rt.download_f32(xt)
+    assert max_rel(_branch(got, x), _branch(exp, x)) <= BLOCK_TOL * 10
+    assert max_rel(got, exp) <= BLOCK_TOL
+
+
+def test_encoder_with_late_blocks_vs_oracle(rt):
+    """Four layers, the last two DA3 late blocks (Q/K LayerNorm), 2 images."""
+    T, layers, images = 865, 4, 2
+    ws = [da3.block_weights(seed=23, layer=l, qk_norm=l >= 2) for l in range(layers)]
+    x = seeded.normal(2300, images * T * 768)
+    pos = da3.positions_yx(24, 36)
+    exp = O.encoder(x, ws, images, T, pos)
+    blocks = [rt.prepare_block(w) for w in ws]
+    fused = rt.upload_f32(x)
+    rt.encoder_run(blocks, fused, images, T, pos)
+    got = rt.download_f32(fused)
+    assert max_rel(got, exp) <= ENCODER_TOL
+    step = rt.upload_f32(x)
+    for b in blocks:
+        rt.vit_block_run(b, step, images, T, pos)
+    assert np.array_equal(got.view(np.uint32), rt.download_f32(step).view(np.uint32))
+
+
+def test_late_block_needs_all_four_qk_norm_vectors(rt):
+    w = da3.block_weights(seed=25, qk_norm=True)
+    del w["k_norm_beta"]
+    with pytest.raises(vh.InvalidArgument):
+        rt.prepare_block(w)

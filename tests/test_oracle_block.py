@@ -1,9 +1,10 @@
 """Pins the oracle's DA3-BASE block composition against an independent
 float64 transcription of the pre-LN ViT block: LN ->
-QKV (+bias) -> 2-D RoPE on Q, K -> softmax(QK^T/8)V -> out-proj (+bias)
-* LayerScale + residual -> LN -> fc1 (+bias) -> exact-erf GELU -> fc2
-(+bias) * LayerScale + residual.  A wrong head split, RoPE axis, missing
-bias or misplaced LayerScale shows up far above the float32 noise here."""
+QKV (+bias) -> [late blocks: LayerNorm of each 64-wide Q/K head row] ->
+2-D RoPE on Q, K -> softmax(QK^T/8)V -> out-proj (+bias) * LayerScale +
+residual -> LN -> fc1 (+bias) -> exact-erf GELU -> fc2 (+bias) * LayerScale
++ residual.  A wrong head split, RoPE axis, missing bias or misplaced
+LayerScale shows up far above the float32 noise here."""
 import math
 
 import numpy as np
@@ -27,6 +28,9 @@ def block64(x, w, T, pos, eps=1e-6, freq=100.0):
     h = ln(x, f["ln1_gamma"], f["ln1_beta"])
     qkv = h @ f["w_qkv"].reshape(D, 3 * D) + f["b_qkv"]
     q, k, v = (qkv[:, i * D:(i + 1) * D].reshape(T, H, 64).transpose(1, 0, 2) for i in range(3))
+    if "q_norm_gamma" in f:  # DA3 late block: LayerNorm of each 64-wide head row
+        q = ln(q.reshape(-1, 64), f["q_norm_gamma"], f["q_norm_beta"]).reshape(H, T, 64)
+        k = ln(k.reshape(-1, 64), f["k_norm_gamma"], f["k_norm_beta"]).reshape(H, T, 64)
     if pos is not None:
         theta = np.float32(freq) ** (-2.0 * np.arange(16) / 32.0)
         p = pos.reshape(T, 2).astype(np.float64)
@@ -94,3 +98,22 @@ def test_layerscale_1e5_keeps_residual_near_identity():
     x = seeded.normal(18, T * 768)
     y = O.vit_block(x, w, 1, T, da3.positions_yx(2, 3))
     assert 0 < np.abs(y - x).max() < 1e-3
+
+
+@pytest.mark.parametrize("layout", ["local", "global", "none"])
+def test_late_block_qk_norm_matches_float64_transcription(layout):
+    """DA3 late blocks (src/specialized.rs:278-316): Q/K LayerNorm before the
+    RoPE, with the local layout, the global layout (every patch at (1, 1),
+    src/specialized.rs:353-358) and without positions."""
+    rows, cols = 3, 4
+    T = rows * cols + 1
+    w = da3.block_weights(seed=19, layerscale=1.0, qk_norm=True)
+    x = seeded.normal(20, T * 768)
+    pos = {"local": da3.positions_yx(rows, cols), "global": da3.positions_global(rows, cols),
+           "none": None}[layout]
+    got, taps = O.vit_block(x, w, 1, T, pos, taps=True)
+    ref, ref_att = block64(x, w, T, pos)
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-5
+    assert np.abs(taps["attn"] - ref_att).max() / np.abs(ref_att).max() < 1e-5
+    plain = O.vit_block(x, {k: v for k, v in w.items() if "norm" not in k or "ln" in k}, 1, T, pos)
+    assert np.abs(plain - got).max() > 1e-3  # the norm is really applied

@@ -170,13 +170,14 @@ struct vh_block {
     Rt rt;
     Lin qkv, proj, fc1, fc2;
     float *ln1_g = nullptr, *ln1_b = nullptr, *ln2_g = nullptr, *ln2_b = nullptr;
+    float *qn_g = nullptr, *qn_b = nullptr, *kn_g = nullptr, *kn_b = nullptr;  // late blocks
     ~vh_block() {
         if (!rt) return;
         hipSetDevice(rt->device);
         for (Lin *l : {&qkv, &proj, &fc1, &fc2})
             for (float *p : {l->wt, l->bias, l->gamma})
                 if (p) hipFreeAsync(p, rt->stream);
-        for (float *p : {ln1_g, ln1_b, ln2_g, ln2_b})
+        for (float *p : {ln1_g, ln1_b, ln2_g, ln2_b, qn_g, qn_b, kn_g, kn_b})
             if (p) hipFreeAsync(p, rt->stream);
     }
 };
@@ -1445,12 +1446,29 @@ vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size
     float *h = ws, *q = h + M * D, *k = q + M * D, *v = k + M * D, *att = v + M * D,
           *f = att + M * D;
     const float *rot = nullptr;
-    if (pos) TRY(rope_table(s, pos, tokens, 64, freq, &rot));
+    if (pos) {
+        TRY(rope_table(s, pos, tokens, 64, freq, &rot));
+    } else if (b.qn_g) {
+        // A late block without positions: every token at (0, 0), whose
+        // rotation (sin 0, cos 1) leaves the normalised rows unchanged.
+        std::vector<int64_t> zero(tokens * 2, 0);
+        TRY(rope_table(s, zero.data(), tokens, 64, freq, &rot));
+    }
     if (!h_ready)
         TRY(launch(s, "layernorm", [&] {
             return vh::launch_layernorm(s.stream, x, b.ln1_g, b.ln1_b, h, M, D, eps);
         }));
-    TRY(run_qkv(s, b.qkv, h, images, tokens, kHeads, rot, q, k, v));
+    if (b.qn_g) {
+        // Late block: QKV with bias only, then LayerNorm of every 64-wide Q
+        // and K head row fused with the RoPE (src/specialized.rs:278-316).
+        TRY(run_qkv(s, b.qkv, h, images, tokens, kHeads, nullptr, q, k, v));
+        TRY(launch(s, "qk_norm_rope", [&] {
+            return vh::launch_qk_norm_rope(s.stream, q, k, b.qn_g, b.qn_b, b.kn_g, b.kn_b, rot,
+                                           M * kHeads, tokens, eps);
+        }));
+    } else {
+        TRY(run_qkv(s, b.qkv, h, images, tokens, kHeads, rot, q, k, v));
+    }
     TRY(flash(s, q, k, v, att, images * kHeads, tokens, kHeads, true));
     const RowNorm ln2{b.ln2_g, b.ln2_b, h, eps};
     TRY(run_lin(s, b.proj, att, M, vh::Epi::Residual, x, "gemm_proj_residual_ln", &ln2));
@@ -1482,6 +1500,10 @@ extern "C" vh_status vh_block_prepare(const vh_runtime *rt, const vh_block_param
                           p->b_fc1,     p->w_fc2,    p->b_fc2, p->ls2};
     for (const float *r : req)
         if (!r) return null_arg("vh_block_prepare parameter");
+    const int qk_norm = !!p->q_norm_gamma + !!p->q_norm_beta + !!p->k_norm_gamma + !!p->k_norm_beta;
+    if (qk_norm != 0 && qk_norm != 4)
+        return fail(VH_ERR_INVALID_ARGUMENT,
+                    "vh_block_prepare: give all four Q/K LayerNorm vectors or none");
     GUARD_BEGIN
     RtState &s = *rt->s;
     TRY(set_device(s));
@@ -1495,6 +1517,12 @@ extern "C" vh_status vh_block_prepare(const vh_runtime *rt, const vh_block_param
     if (!st) st = upload_small(s, p->ln1_beta, kDim, &b->ln1_b, "ln1 beta");
     if (!st) st = upload_small(s, p->ln2_gamma, kDim, &b->ln2_g, "ln2 gamma");
     if (!st) st = upload_small(s, p->ln2_beta, kDim, &b->ln2_b, "ln2 beta");
+    if (qk_norm) {
+        if (!st) st = upload_small(s, p->q_norm_gamma, 64, &b->qn_g, "q norm gamma");
+        if (!st) st = upload_small(s, p->q_norm_beta, 64, &b->qn_b, "q norm beta");
+        if (!st) st = upload_small(s, p->k_norm_gamma, 64, &b->kn_g, "k norm gamma");
+        if (!st) st = upload_small(s, p->k_norm_beta, 64, &b->kn_b, "k norm beta");
+    }
     if (st) {
         delete b;
         return st;

@@ -299,7 +299,7 @@ class Q8Tensor:
 
 
 class BlockParams(ctypes.Structure):
-    _fields_ = [(n, _f32p) for n in da3.BLOCK_FIELDS]
+    _fields_ = [(n, _f32p) for n in da3.BLOCK_FIELDS + da3.QK_NORM_FIELDS]
 
 
 class Block:
@@ -482,7 +482,8 @@ class Runtime:
 
     # -- DA3 block / encoder
     def prepare_block(self, weights: dict) -> Block:
-        keep = {n: _f32(weights[n]).reshape(-1) for n in da3.BLOCK_FIELDS}
+        keep = {n: _f32(weights[n]).reshape(-1) for n in da3.BLOCK_FIELDS + da3.QK_NORM_FIELDS
+                if weights.get(n) is not None}
         params = BlockParams(**{n: _fp(a) for n, a in keep.items()})
         out = ctypes.c_void_p()
         _check(lib().vh_block_prepare(self._h, ctypes.byref(params), ctypes.byref(out)))

@@ -23,6 +23,8 @@ LAYERSCALE = 1e-5
 
 BLOCK_FIELDS = ("ln1_gamma", "ln1_beta", "w_qkv", "b_qkv", "w_proj", "b_proj", "ls1",
                 "ln2_gamma", "ln2_beta", "w_fc1", "b_fc1", "w_fc2", "b_fc2", "ls2")
+# DA3 late blocks only (Q/K LayerNorm before the RoPE); absent for plain blocks.
+QK_NORM_FIELDS = ("q_norm_gamma", "q_norm_beta", "k_norm_gamma", "k_norm_beta")
 
 
 def grid(height_px: int, width_px: int) -> tuple[int, int]:
@@ -54,13 +56,24 @@ def positions_global(rows: int, cols: int, special: int = 1) -> np.ndarray:
 
 
 def block_weights(seed: int, layer: int = 0, layerscale: float = LAYERSCALE,
-                  w_std: float = 0.02, b_std: float = 0.02) -> dict[str, np.ndarray]:
+                  w_std: float = 0.02, b_std: float = 0.02,
+                  qk_norm: bool = False) -> dict[str, np.ndarray]:
     """Seeded block parameters: weights N(0, w_std^2) row-major [in, out],
-    biases N(0, b_std^2), LayerNorm gamma=1 / beta=0, LayerScale constant."""
+    biases N(0, b_std^2), LayerNorm gamma=1 / beta=0, LayerScale constant.
+    With qk_norm (DA3's late blocks) the 64-wide Q and K LayerNorms get
+    gamma ~ 1 + N(0, 0.1^2) and beta ~ N(0, b_std^2)."""
     def n(tid, count, std):
         return seeded.normal(seeded.tensor_seed(seed, layer, tid), count, std)
 
-    return {
+    extra = {}
+    if qk_norm:
+        extra = {
+            "q_norm_gamma": (1.0 + n(9, HEAD_DIM, 0.1)).astype(np.float32),
+            "q_norm_beta": n(10, HEAD_DIM, b_std),
+            "k_norm_gamma": (1.0 + n(11, HEAD_DIM, 0.1)).astype(np.float32),
+            "k_norm_beta": n(12, HEAD_DIM, b_std),
+        }
+    return extra | {
         "ln1_gamma": np.ones(DIM, np.float32),
         "ln1_beta": np.zeros(DIM, np.float32),
         "w_qkv": n(1, DIM * QKV, w_std),
