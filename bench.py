@@ -148,6 +148,51 @@ def gpu_q8_0(steps: int) -> dict:
             "quantize_gbs": round(quant_bytes / (q_us * 1e-6) / 1e9, 1)}
 
 
+def gpu_elementwise(reps: int = 20) -> dict:
+    """The bandwidth-bound kernels at sizes where bandwidth, not launch
+    latency, decides: LayerNorm over 4 x 865 tokens, GELU over the batched
+    fc1 output, and the residual add over 16 Mi floats.  Per-launch HIP
+    event timing; bytes are the algorithmic reads plus writes."""
+    import vestra_hip as vh
+    from vestra_hip import seeded
+
+    rt = vh.Runtime(0)
+    rows = 4 * T
+    x = rt.upload_f32(seeded.normal(31, rows * D))
+    g = rt.upload_f32(np.ones(D, np.float32))
+    b = rt.upload_f32(np.zeros(D, np.float32))
+    f = rt.upload_f32(seeded.normal(32, rows * F))
+    n_add = 16 * 1024 * 1024
+    a1 = rt.upload_f32(np.ones(n_add, np.float32))
+    a2 = rt.upload_f32(np.ones(n_add, np.float32))
+    for _ in range(3):
+        rt.layernorm_f32(x, g, b, rows, D, 1e-6)
+        rt.gelu_f32_in_place(f)
+        rt.add_f32_in_place(a1, a2)
+    rt.synchronize()
+    rt.profile_reset()
+    rt.profile_enable(True)
+    keep = []
+    for _ in range(reps):
+        keep.append(rt.layernorm_f32(x, g, b, rows, D, 1e-6))
+        rt.gelu_f32_in_place(f)
+        rt.add_f32_in_place(a1, a2)
+    prof = rt.profile_report()
+    rt.profile_enable(False)
+    del keep
+    sizes = {"layernorm": (2 * rows * D * 4 + 2 * D * 4, f"{rows}x{D}"),
+             "gelu": (2 * rows * F * 4, f"{rows}x{F}"),
+             "add": (3 * n_add * 4, f"{n_add}")}
+    out = {}
+    for name, (nbytes, shape) in sizes.items():
+        us = 1e3 * prof[name][1] / prof[name][0]
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"shape": shape, "us": round(us, 2), "gbs": round(gbs, 1),
+                     "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+        log(f"  {name:10s} {shape:>10s} {us:8.2f} us {gbs:8.1f} GB/s")
+    return out
+
+
 def cpu_block(budget_s: float) -> dict:
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
@@ -195,6 +240,7 @@ def main() -> int:
 
     gpu = gpu_block(args.steps, args.warmup)
     q8 = gpu_q8_0(max(10, min(args.steps, 100)))
+    elementwise = gpu_elementwise()
     if args.calibrate:
         import vestra_hip as vh
 
@@ -240,6 +286,7 @@ def main() -> int:
         },
         "kernels": ker,
         "q8_0": q8,
+        "elementwise_at_scale": elementwise,
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_block(args.cpu_seconds)

@@ -59,6 +59,20 @@ __global__ void gelu_kernel(float *__restrict__ v, size_t n) {
     }
 }
 
+// Four values per thread with 16-byte accesses (v 16-byte aligned, n % 4 ==
+// 0); every element takes the same form as in gelu_kernel.
+__global__ __launch_bounds__(256) void gelu4_kernel(float *__restrict__ v, size_t n4, size_t main) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    f32x4 *v4 = reinterpret_cast<f32x4 *>(v);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        f32x4 x = v4[i];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            x[e] = 4 * i + e < main ? gelu_avx512_form(x[e]) : gelu_scalar_form(x[e]);
+        v4[i] = x;
+    }
+}
+
 // One wave64 per row; up to 4 float4 per lane stay in registers (cols <= 1024
 // and cols % 4 == 0), otherwise the row is re-read.  Tree reductions differ
 // from the sequential CPU sums only in rounding (tolerance-checked).
@@ -321,7 +335,10 @@ hipError_t launch_bias_scale(hipStream_t s, float *v, const float *bias, const f
 
 hipError_t launch_gelu(hipStream_t s, float *v, size_t n) {
     if (n == 0) return hipSuccess;
-    gelu_kernel<<<grid_for(n), kThreads, 0, s>>>(v, n);
+    if (n % 4 == 0 && (reinterpret_cast<uintptr_t>(v) & 15) == 0)
+        gelu4_kernel<<<grid_for(n / 4), 256, 0, s>>>(v, n / 4, n - n % 16);
+    else
+        gelu_kernel<<<grid_for(n), kThreads, 0, s>>>(v, n);
     return hipGetLastError();
 }
 
