@@ -51,9 +51,25 @@ __device__ __forceinline__ float div_rn(float a, float b) {
 // 53 >= 2*24 + 2 makes double rounding innocuous for sqrt.
 __device__ __forceinline__ float sqrt_rn(float x) { return (float)__builtin_sqrt((double)x); }
 
+// One DPP lane permutation (a VALU modifier, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+
+// Butterfly sum over the 64 lanes; every lane ends with the same total
+// (each step adds two group sums, and a + b == b + a).  Within a 16-lane
+// row by DPP: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
+// row_half_mirror (pairs the two quads of each 8), row_mirror (pairs the two
+// 8s of each 16); across rows by two shuffles.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    v += dpp_f32<0xb1>(v);
+    v += dpp_f32<0x4e>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    v += __shfl_xor(v, 16, kWave);
+    v += __shfl_xor(v, 32, kWave);
     return v;
 }
 
