@@ -47,6 +47,7 @@ typedef struct vh_tensor vh_tensor;       /* CudaTensorF32 (src/cuda.rs:1283-128
 typedef struct vh_linear vh_linear;       /* CudaLinearF32 (src/cuda.rs:1291-1298) */
 typedef struct vh_q8_tensor vh_q8_tensor; /* device rows of BlockQ8_0 (src/lib.rs:33-38) */
 typedef struct vh_block vh_block;         /* prepared DA3-BASE encoder block */
+typedef struct vh_linear_q8 vh_linear_q8; /* projection with BlockQ8_0 weights */
 
 /* ---- errors --------------------------------------------------------------- */
 /* Message of the calling thread's last failure ("" if none). */
@@ -217,6 +218,32 @@ vh_status vh_quantize_q8_0(const vh_runtime *rt, const vh_tensor *x, size_t rows
 vh_status vh_gemm_q8_0(const vh_runtime *rt, const vh_q8_tensor *a_q, const vh_q8_tensor *b_q,
                        size_t m, size_t n, size_t k, vh_tensor **out);
 
+/* ---- Q8_0 projections -------------------------------------------------------- */
+/* A projection whose weights are GGUF-style BlockQ8_0 (src/lib.rs:33-38): the
+ * pre-transposed row blocks that Kernels::gemm_q8_0 takes as its b operand
+ * (src/dispatch.rs:91-105), output_features rows of input_features/32 blocks,
+ * repacked block-major at prepare time.  bias and gamma ([N]) may be NULL.
+ * Each run quantises the f32 input rows on the device (quantize_row_q8_0,
+ * src/q8_0_dot.rs:27-46), forms the exact block-dot sums, and applies the
+ * f32 epilogue as the engine's separate passes would (src/scalar.rs:65-81
+ * add_bias_rows, src/scalar.rs:139-155 layerscale, src/dispatch.rs:56-83 gelu
+ * and add), each op rounded as there.  Bit-exact with that composition. */
+vh_status vh_prepare_linear_q8_0(const vh_runtime *rt, size_t input_features,
+                                 size_t output_features, const void *weight_blocks,
+                                 const float *bias, const float *gamma, vh_linear_q8 **out);
+void vh_linear_q8_0_free(vh_linear_q8 *linear);
+size_t vh_linear_q8_0_input_features(const vh_linear_q8 *linear);
+size_t vh_linear_q8_0_output_features(const vh_linear_q8 *linear);
+/* out = (gemm_q8_0(quantize(input), W) + bias) * gamma */
+vh_status vh_linear_q8_0_run(const vh_linear_q8 *linear, const vh_tensor *input, size_t rows,
+                             vh_tensor **out);
+/* out = gelu(gemm_q8_0(quantize(input), W) + bias); gamma must be NULL. */
+vh_status vh_linear_q8_0_run_gelu(const vh_linear_q8 *linear, const vh_tensor *input,
+                                  size_t rows, vh_tensor **out);
+/* residual += (gemm_q8_0(quantize(input), W) + bias) * gamma */
+vh_status vh_linear_q8_0_run_residual(const vh_linear_q8 *linear, const vh_tensor *input,
+                                      size_t rows, vh_tensor *residual);
+
 /* ---- DA3-BASE encoder block ------------------------------------------------ */
 /* Host pointers to one block's parameters, row-major [in, out] weights. */
 typedef struct vh_block_params {
@@ -236,6 +263,15 @@ typedef struct vh_block_params {
 
 /* Uploads and repacks one block's weights (model-load time). */
 vh_status vh_block_prepare(const vh_runtime *rt, const vh_block_params *params, vh_block **out);
+/* The same block with its four projections in Q8_0: each f32 weight W [in, out]
+ * is quantised on the device as the rows of W^T (quantize_row_q8_0,
+ * src/q8_0_dot.rs:27-46), and every projection quantises its input rows and
+ * runs the block-dot GEMM of vh_linear_q8_0_run.  The crate has no Q8_0
+ * block; this one follows the same engine composition with
+ * Kernels::gemm_q8_0 (src/dispatch.rs:91-105) in place of each f32 GEMM. */
+vh_status vh_block_prepare_q8_0(const vh_runtime *rt, const vh_block_params *params,
+                                vh_block **out);
+int vh_block_is_q8_0(const vh_block *block);
 void vh_block_free(vh_block *block);
 /* One pre-LN DA3-BASE block in place on x [images*tokens*768]: LN, QKV (+bias,
  * + 2-D RoPE when pos_yx != NULL; a late block first normalises each Q and K

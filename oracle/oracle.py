@@ -85,8 +85,9 @@ def _declare(L):
     sig("vko_qkv", None, _sz, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p)
     sig("vko_split_qkv_hnd", None, _f32p, _sz, _sz, _sz, _f32p, _f32p, _f32p)
     sig("vko_hnd_to_token", None, _f32p, _sz, _sz, _sz, _f32p)
-    sig("vko_vit_block", None, _f32p, _sz, _sz, ctypes.POINTER(BlockWeights), _i64p,
-        ctypes.c_float, ctypes.c_float, _f32p, _f32p, _f32p)
+    for name in ("vko_vit_block", "vko_vit_block_q8_0"):
+        sig(name, None, _f32p, _sz, _sz, ctypes.POINTER(BlockWeights), _i64p,
+            ctypes.c_float, ctypes.c_float, _f32p, _f32p, _f32p)
 
 
 class BlockWeights(ctypes.Structure):
@@ -373,8 +374,12 @@ BLOCK_FIELDS = [f for f, _ in BlockWeights._fields_ if f not in QK_NORM_FIELDS]
 
 
 def vit_block(x, weights: dict, images, tokens, pos_yx=None, rope_freq=100.0, eps=1e-6,
-              taps=False):
-    """One DA3-BASE encoder block per image (engine composition of the crate's kernels)."""
+              taps=False, q8_0=False):
+    """One DA3-BASE encoder block per image (engine composition of the crate's kernels).
+
+    q8_0=True runs the four projections as Q8_0: quantize_row_q8_0 of the
+    input rows and of the rows of W^T, Kernels::gemm_q8_0, then bias /
+    LayerScale / GELU as separate f32 passes (vko_vit_block_q8_0)."""
     xs = f32(x).copy()
     keep = {n: f32(weights[n]) for n in BLOCK_FIELDS + QK_NORM_FIELDS if weights.get(n) is not None}
     bw = BlockWeights(**{n: _f(a) for n, a in keep.items()})
@@ -385,17 +390,19 @@ def vit_block(x, weights: dict, images, tokens, pos_yx=None, rope_freq=100.0, ep
         t_ln = np.empty(images * tokens * 768, np.float32)
         t_att = np.empty(images * tokens * 768, np.float32)
         t_gelu = np.empty(images * tokens * 3072, np.float32)
-    lib().vko_vit_block(_f(xs), images, tokens, ctypes.byref(bw),
-                        _i(pos) if pos is not None else ctypes.cast(None, _i64p),
-                        rope_freq, eps,
-                        _f(t_ln) if taps else null, _f(t_att) if taps else null,
-                        _f(t_gelu) if taps else null)
+    fn = lib().vko_vit_block_q8_0 if q8_0 else lib().vko_vit_block
+    fn(_f(xs), images, tokens, ctypes.byref(bw),
+       _i(pos) if pos is not None else ctypes.cast(None, _i64p), rope_freq, eps,
+       _f(t_ln) if taps else null, _f(t_att) if taps else null, _f(t_gelu) if taps else null)
     if taps:
         return xs, {"ln1": t_ln, "attn": t_att, "gelu": t_gelu}
     return xs
 
 
-def encoder(x, layers: list, images, tokens, pos_yx=None, rope_freq=100.0, eps=1e-6):
-    for w in layers:
-        x = vit_block(x, w, images, tokens, pos_yx, rope_freq, eps)
+def encoder(x, layers: list, images, tokens, pos_yx=None, rope_freq=100.0, eps=1e-6,
+            q8_0=False):
+    """Blocks in order; q8_0 is one flag for all or a list with one per block."""
+    flags = q8_0 if isinstance(q8_0, (list, tuple)) else [q8_0] * len(layers)
+    for w, q in zip(layers, flags):
+        x = vit_block(x, w, images, tokens, pos_yx, rope_freq, eps, q8_0=q)
     return x

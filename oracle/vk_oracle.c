@@ -1137,14 +1137,45 @@ void vko_hnd_to_token(const float *hnd, size_t tokens, size_t heads, size_t hd, 
 }
 
 /* ------------------------------------------------------------------------ */
-/* DA3-BASE ViT block (engine composition; SURVEY call stack A)             */
+/* DA3-BASE ViT block (the engine composition of the crate kernels)         */
 /* ------------------------------------------------------------------------ */
 
-void vko_vit_block(float *x_all, size_t images, size_t tokens, const vko_block_weights *w,
-                   const int64_t *pos_yx, float rope_freq, float eps, float *tap_ln1,
-                   float *tap_attn, float *tap_gelu) {
+/* Q8_0 blocks of W^T for W [k][n] row-major: quantize_row_q8_0 of each of
+ * the n columns, the pre-transposed row-block operand of Kernels::gemm_q8_0
+ * (src/scalar.rs:25-56). */
+static vko_block_q8_0 *q8_weight(const float *w, size_t k, size_t n) {
+    float *wt = (float *)malloc(k * n * sizeof(float));
+    vko_block_q8_0 *q = (vko_block_q8_0 *)malloc(n * (k / 32) * sizeof(vko_block_q8_0));
+    for (size_t i = 0; i < k; i++)
+        for (size_t j = 0; j < n; j++) wt[j * k + i] = w[i * n + j];
+    vko_quantize_row_q8_0(wt, n * (k / 32), q);
+    free(wt);
+    return q;
+}
+
+/* c [m][n] = Kernels::gemm_q8_0(quantize_row_q8_0(a rows), wq) */
+static void q8_project(size_t m, size_t n, size_t k, const float *a, const vko_block_q8_0 *wq,
+                       float *c) {
+    vko_block_q8_0 *aq = (vko_block_q8_0 *)malloc(m * (k / 32) * sizeof(vko_block_q8_0));
+    vko_quantize_row_q8_0(a, m * (k / 32), aq);
+    vko_kernels_gemm_q8_0(m, n, k, aq, wq, c);
+    free(aq);
+}
+
+static void vit_block_impl(float *x_all, size_t images, size_t tokens,
+                           const vko_block_weights *w, const int64_t *pos_yx, float rope_freq,
+                           float eps, float *tap_ln1, float *tap_attn, float *tap_gelu, int q8) {
     const size_t D = 768, H = 12, F = 3072;
     size_t T = tokens;
+    vko_block_q8_0 *wq_qkv = NULL, *wq_proj = NULL, *wq_fc1 = NULL, *wq_fc2 = NULL;
+    float *qkv = NULL;
+    if (q8) {
+        wq_qkv = q8_weight(w->w_qkv, D, 3 * D);
+        wq_proj = q8_weight(w->w_proj, D, D);
+        wq_fc1 = q8_weight(w->w_fc1, D, F);
+        wq_fc2 = q8_weight(w->w_fc2, F, D);
+        qkv = (float *)malloc(T * 3 * D * sizeof(float));
+    }
     float *h = (float *)malloc(T * D * sizeof(float));
     float *qb = (float *)malloc(T * D * sizeof(float));
     float *kb = (float *)malloc(T * D * sizeof(float));
@@ -1159,8 +1190,15 @@ void vko_vit_block(float *x_all, size_t images, size_t tokens, const vko_block_w
         memcpy(h, x, T * D * sizeof(float));
         vko_layernorm(h, T, D, w->ln1_gamma, w->ln1_beta, eps);
         if (tap_ln1) memcpy(tap_ln1 + img * T * D, h, T * D * sizeof(float));
-        /* QKV with bias, head-major (src/specialized.rs:996) */
-        vko_qkv(T, h, w->w_qkv, w->b_qkv, qb, kb, vb);
+        if (q8) {
+            /* Q8_0 QKV, then add_bias_rows, then the head-major split */
+            q8_project(T, 3 * D, D, h, wq_qkv, qkv);
+            vko_add_bias_rows(qkv, T, 3 * D, w->b_qkv);
+            vko_split_qkv_hnd(qkv, T, H, 64, qb, kb, vb);
+        } else {
+            /* QKV with bias, head-major (src/specialized.rs:996) */
+            vko_qkv(T, h, w->w_qkv, w->b_qkv, qb, kb, vb);
+        }
         if (w->q_norm_gamma) {
             /* late block: Q/K LayerNorm fused with the RoPE
              * (src/specialized.rs:278-316); without positions every token
@@ -1180,18 +1218,39 @@ void vko_vit_block(float *x_all, size_t images, size_t tokens, const vko_block_w
         vko_hnd_to_token(ob, T, H, 64, att);
         if (tap_attn) memcpy(tap_attn + img * T * D, att, T * D * sizeof(float));
         /* out-projection + LayerScale, residual (src/specialized.rs:811, dispatch.rs:77) */
-        vko_linear_bias_scale(T, D, D, att, w->w_proj, w->b_proj, w->ls1, y);
+        if (q8) {
+            /* (acc + bias) * ls: add_bias_rows then layerscale */
+            q8_project(T, D, D, att, wq_proj, y);
+            vko_add_bias_rows(y, T, D, w->b_proj);
+            vko_layerscale(y, T, D, w->ls1);
+        } else {
+            vko_linear_bias_scale(T, D, D, att, w->w_proj, w->b_proj, w->ls1, y);
+        }
         vko_kernels_add(x, y, T * D);
         /* MLP */
         memcpy(h, x, T * D * sizeof(float));
         vko_layernorm(h, T, D, w->ln2_gamma, w->ln2_beta, eps);
-        vko_linear(T, F, D, h, w->w_fc1, f);
+        if (q8)
+            q8_project(T, F, D, h, wq_fc1, f);
+        else
+            vko_linear(T, F, D, h, w->w_fc1, f);
         vko_add_bias_rows(f, T, F, w->b_fc1);
         vko_kernels_gelu(f, T * F);
         if (tap_gelu) memcpy(tap_gelu + img * T * F, f, T * F * sizeof(float));
-        vko_linear_bias_scale(T, D, F, f, w->w_fc2, w->b_fc2, w->ls2, y);
+        if (q8) {
+            q8_project(T, D, F, f, wq_fc2, y);
+            vko_add_bias_rows(y, T, D, w->b_fc2);
+            vko_layerscale(y, T, D, w->ls2);
+        } else {
+            vko_linear_bias_scale(T, D, F, f, w->w_fc2, w->b_fc2, w->ls2, y);
+        }
         vko_kernels_add(x, y, T * D);
     }
+    free(wq_qkv);
+    free(wq_proj);
+    free(wq_fc1);
+    free(wq_fc2);
+    free(qkv);
     free(h);
     free(qb);
     free(kb);
@@ -1200,4 +1259,18 @@ void vko_vit_block(float *x_all, size_t images, size_t tokens, const vko_block_w
     free(att);
     free(y);
     free(f);
+}
+
+void vko_vit_block(float *x_all, size_t images, size_t tokens, const vko_block_weights *w,
+                   const int64_t *pos_yx, float rope_freq, float eps, float *tap_ln1,
+                   float *tap_attn, float *tap_gelu) {
+    vit_block_impl(x_all, images, tokens, w, pos_yx, rope_freq, eps, tap_ln1, tap_attn, tap_gelu,
+                   0);
+}
+
+void vko_vit_block_q8_0(float *x_all, size_t images, size_t tokens, const vko_block_weights *w,
+                        const int64_t *pos_yx, float rope_freq, float eps, float *tap_ln1,
+                        float *tap_attn, float *tap_gelu) {
+    vit_block_impl(x_all, images, tokens, w, pos_yx, rope_freq, eps, tap_ln1, tap_attn, tap_gelu,
+                   1);
 }

@@ -141,6 +141,16 @@ typedef struct vko_block_weights {
 void vko_vit_block(float *x, size_t images, size_t tokens, const vko_block_weights *w,
                    const int64_t *pos_yx, float rope_freq, float eps, float *tap_ln1,
                    float *tap_attn, float *tap_gelu);
+/* The same block with Q8_0 projections: every projection input is quantised
+ * with quantize_row_q8_0 (src/q8_0_dot.rs:27-46), each weight W [k][n] as the
+ * rows of W^T, the product is Kernels::gemm_q8_0 (src/dispatch.rs:91-105),
+ * and bias / LayerScale / GELU follow as separate f32 passes
+ * (add_bias_rows, layerscale, Kernels::gelu).  The QKV product gets its bias
+ * and is then split head-major.  The engine-level composition is this
+ * backend's own; the crate has no Q8_0 block. */
+void vko_vit_block_q8_0(float *x, size_t images, size_t tokens, const vko_block_weights *w,
+                        const int64_t *pos_yx, float rope_freq, float eps, float *tap_ln1,
+                        float *tap_attn, float *tap_gelu);
 
 #ifdef __cplusplus
 }

@@ -70,12 +70,23 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
 constexpr int QCH = 32;  // blocks per scale chunk (a multiple of QPF)
 constexpr int QPF = 4;   // prefetch distance in blocks
 
+// Epilogue of a Q8_0 projection, applied to the exact block-order sum with
+// separately rounded ops (the f32 ops the engine applies after
+// Kernels::gemm_q8_0): Store c = (acc + bias) * gamma; Gelu c = gelu(acc +
+// bias) (AVX-512 form below tail_start, scalar form after); Residual
+// c = c + (acc + bias) * gamma.  bias / gamma may be null.
+struct Q8Epi {
+    const float *bias, *gamma;
+    size_t tail_start;
+};
+
+template <Epi EPI>
 __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict__ a_qs,
                                                         const uint16_t *__restrict__ a_d,
                                                         const int8_t *__restrict__ b_qs,
                                                         const uint16_t *__restrict__ b_d,
                                                         float *__restrict__ c, int M, int N,
-                                                        int K) {
+                                                        int K, Q8Epi ep) {
     __shared__ __attribute__((aligned(16))) float sa[QCH][64];
     __shared__ __attribute__((aligned(16))) float sb[QCH][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -156,6 +167,25 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
             }
         }
     }
+    // Epilogue reads (bias, gamma, residual) from clamped indices before any
+    // store, so that they overlap.
+    float bias[2], gamma[2], resid[2][2][4];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int col = min(nw + j * 16 + li, N - 1);
+        bias[j] = ep.bias ? ep.bias[col] : 0.0f;
+        gamma[j] = ep.gamma ? ep.gamma[col] : 1.0f;
+    }
+    if constexpr (EPI == Epi::Residual) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    resid[i][j][r] = c[(size_t)min(mw + i * 16 + 4 * lh + r, M - 1) * N +
+                                       min(nw + j * 16 + li, N - 1)];
+    }
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -165,7 +195,16 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int row = mw + i * 16 + 4 * lh + r;
-                if (row < M) c[(size_t)row * N + col] = acc[i][j][r];
+                if (row >= M) continue;
+                const size_t idx = (size_t)row * N + col;
+                float v = acc[i][j][r];
+                if (ep.bias) v = add_rn(v, bias[j]);
+                if constexpr (EPI == Epi::Gelu) {
+                    c[idx] = idx < ep.tail_start ? gelu_avx512_form(v) : gelu_scalar_form(v);
+                } else {
+                    if (ep.gamma) v = mul_rn(v, gamma[j]);
+                    c[idx] = EPI == Epi::Residual ? add_rn(resid[i][j][r], v) : v;
+                }
             }
         }
 }
@@ -183,10 +222,17 @@ hipError_t launch_quantize_q8_0(hipStream_t s, const float *x, int8_t *qs, uint1
 
 hipError_t launch_gemm_q8_0(hipStream_t s, const int8_t *a_qs, const uint16_t *a_d,
                             const int8_t *b_qs, const uint16_t *b_d, float *c, size_t m,
-                            size_t n, size_t k) {
+                            size_t n, size_t k, Epi epi, const float *bias, const float *gamma) {
     if (m == 0 || n == 0) return hipSuccess;
     dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64));
-    gemm_q8_0_kernel<<<grid, 256, 0, s>>>(a_qs, a_d, b_qs, b_d, c, (int)m, (int)n, (int)k);
+    const Q8Epi ep{bias, gamma, m * n - (m * n) % 16};
+    const int M = (int)m, N = (int)n, K = (int)k;
+    switch (epi) {
+        case Epi::Store: gemm_q8_0_kernel<Epi::Store><<<grid, 256, 0, s>>>(a_qs, a_d, b_qs, b_d, c, M, N, K, ep); break;
+        case Epi::Gelu: gemm_q8_0_kernel<Epi::Gelu><<<grid, 256, 0, s>>>(a_qs, a_d, b_qs, b_d, c, M, N, K, ep); break;
+        case Epi::Residual: gemm_q8_0_kernel<Epi::Residual><<<grid, 256, 0, s>>>(a_qs, a_d, b_qs, b_d, c, M, N, K, ep); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

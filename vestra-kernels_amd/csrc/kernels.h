@@ -89,8 +89,11 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs &g);
 // x [rows][k] -> block-major Q8_0: qs [k/32][rows][32] int8, d [k/32][rows] f16 bits
 hipError_t launch_quantize_q8_0(hipStream_t s, const float *x, int8_t *qs, uint16_t *d,
                                 size_t rows, size_t k);
+// c = a . b^T block by block (exact int sums, block-order f32 fold), then the
+// epilogue (Store / Gelu / Residual, see k_q8.hip); bias / gamma may be null.
 hipError_t launch_gemm_q8_0(hipStream_t s, const int8_t *a_qs, const uint16_t *a_d,
                             const int8_t *b_qs, const uint16_t *b_d, float *c, size_t m,
-                            size_t n, size_t k);
+                            size_t n, size_t k, Epi epi = Epi::Store, const float *bias = nullptr,
+                            const float *gamma = nullptr);
 
 }  // namespace vh

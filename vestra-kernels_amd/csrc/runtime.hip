@@ -86,6 +86,8 @@ struct RtState {
     size_t sk_floats = 0;
     float *fw = nullptr;                        // grow-only attention key-split partials
     size_t fw_floats = 0;
+    char *aq = nullptr;                         // grow-only Q8_0 activation blocks
+    size_t aq_bytes = 0;
 
     bool profile = false;
     std::vector<ProfileRec> pending;
@@ -100,6 +102,7 @@ struct RtState {
         if (ws) hipFree(ws);
         if (sk) hipFree(sk);
         if (fw) hipFree(fw);
+        if (aq) hipFree(aq);
 
         for (auto &p : pending) {
             hipEventDestroy(p.a);
@@ -140,6 +143,23 @@ struct Lin {
     float *gamma = nullptr;  // null = unit LayerScale
 };
 
+// A projection with Q8_0 weights: W^T [N][K] as block-major blocks,
+// qs [K/32][N][32] and d [K/32][N] (binary16 bits).
+struct Q8Lin {
+    size_t K = 0, N = 0;
+    int8_t *qs = nullptr;
+    uint16_t *d = nullptr;
+    float *bias = nullptr;
+    float *gamma = nullptr;  // null = unit LayerScale
+    void release(hipStream_t s) {
+        if (qs) hipFreeAsync(qs, s);
+        if (d) hipFreeAsync(d, s);
+        for (float *p : {bias, gamma})
+            if (p) hipFreeAsync(p, s);
+        *this = Q8Lin{};
+    }
+};
+
 }  // namespace
 
 struct vh_linear {
@@ -166,9 +186,21 @@ struct vh_q8_tensor {
     }
 };
 
+struct vh_linear_q8 {
+    Rt rt;
+    Q8Lin L;
+    ~vh_linear_q8() {
+        if (!rt) return;
+        hipSetDevice(rt->device);
+        L.release(rt->stream);
+    }
+};
+
 struct vh_block {
     Rt rt;
     Lin qkv, proj, fc1, fc2;
+    bool q8 = false;  // projections in Q8_0 (qqkv..qfc2) instead of f32
+    Q8Lin qqkv, qproj, qfc1, qfc2;
     float *ln1_g = nullptr, *ln1_b = nullptr, *ln2_g = nullptr, *ln2_b = nullptr;
     float *qn_g = nullptr, *qn_b = nullptr, *kn_g = nullptr, *kn_b = nullptr;  // late blocks
     ~vh_block() {
@@ -177,6 +209,7 @@ struct vh_block {
         for (Lin *l : {&qkv, &proj, &fc1, &fc2})
             for (float *p : {l->wt, l->bias, l->gamma})
                 if (p) hipFreeAsync(p, rt->stream);
+        for (Q8Lin *l : {&qqkv, &qproj, &qfc1, &qfc2}) l->release(rt->stream);
         for (float *p : {ln1_g, ln1_b, ln2_g, ln2_b, qn_g, qn_b, kn_g, kn_b})
             if (p) hipFreeAsync(p, rt->stream);
     }
@@ -422,6 +455,64 @@ vh_status run_qkv(RtState &s, const Lin &L, const float *in, size_t images, size
 }
 
 bool mul_overflows(size_t a, size_t b, size_t *out) { return __builtin_mul_overflow(a, b, out); }
+
+// Block-major Q8_0 blocks of a rows x k activation: qs, then d 256 bytes on.
+vh_status q8_workspace(RtState &s, size_t rows, size_t k, int8_t **qs, uint16_t **d) {
+    const size_t qbytes = (rows * k + 255) & ~size_t(255);
+    const size_t need = qbytes + rows * (k / 32) * sizeof(uint16_t);
+    if (s.aq_bytes < need) {
+        hipStreamSynchronize(s.stream);
+        if (s.aq) hipFree(s.aq);
+        s.aq = nullptr;
+        s.aq_bytes = 0;
+        hipError_t e = hipMalloc(&s.aq, need);
+        if (e != hipSuccess) return fail(VH_ERR_UPLOAD, hip_msg("Q8_0 activation workspace allocation", e));
+        s.aq_bytes = need;
+    }
+    *qs = reinterpret_cast<int8_t *>(s.aq);
+    *d = reinterpret_cast<uint16_t *>(s.aq + qbytes);
+    return VH_OK;
+}
+
+// The engine's Q8_0 projection: quantise the input rows (quantize_row_q8_0),
+// block-dot GEMM against the weight blocks, then the epilogue.
+vh_status run_q8(RtState &s, const Q8Lin &L, const float *in, size_t rows, vh::Epi epi, float *c,
+                 const char *name) {
+    int8_t *qs = nullptr;
+    uint16_t *d = nullptr;
+    TRY(q8_workspace(s, rows, L.K, &qs, &d));
+    TRY(launch(s, "quantize_q8_0", [&] {
+        return vh::launch_quantize_q8_0(s.stream, in, qs, d, rows, L.K);
+    }));
+    return launch(s, name, [&] {
+        return vh::launch_gemm_q8_0(s.stream, qs, d, L.qs, L.d, c, rows, L.N, L.K, epi, L.bias,
+                                    epi == vh::Epi::Gelu ? nullptr : L.gamma);
+    });
+}
+
+// f32 weights [K][N] row-major -> Q8_0 blocks of W^T rows, quantised on the
+// device with the activation kernel (quantize_row_q8_0 of each column).
+vh_status prepare_q8_from_f32(RtState &s, size_t K, size_t N, const float *w, const float *bias,
+                              const float *gamma, Q8Lin *Q) {
+    Lin L;
+    TRY(prepare_lin(s, K, N, w, bias, gamma, &L));
+    vh_status st = dalloc(s, K * N, &Q->qs, "Q8_0 weight allocation");
+    if (!st) st = dalloc(s, N * (K / 32), &Q->d, "Q8_0 weight allocation");
+    if (!st)
+        st = launch(s, "quantize_q8_0", [&] {
+            return vh::launch_quantize_q8_0(s.stream, L.wt, Q->qs, Q->d, N, K);
+        });
+    hipFreeAsync(L.wt, s.stream);
+    Q->bias = L.bias;
+    Q->gamma = L.gamma;
+    if (st) {
+        Q->release(s.stream);
+        return st;
+    }
+    Q->K = K;
+    Q->N = N;
+    return VH_OK;
+}
 
 }  // namespace
 
@@ -1288,6 +1379,23 @@ vh_status new_q8(const Rt &rt, size_t rows, size_t k, vh_q8_tensor **out) {
     *out = t;
     return VH_OK;
 }
+
+// BlockQ8_0 AoS, rows x (k/32) blocks row by row, to block-major arrays: the
+// block of row r and k-slice j goes to slot j * rows + r.
+void unpack_q8_aos(const void *blocks, size_t rows, size_t k, std::vector<int8_t> &qs,
+                   std::vector<uint16_t> &d) {
+    const size_t nbr = k / 32, nb = rows * nbr;
+    qs.resize(nb * 32);
+    d.resize(nb);
+    const BlockQ8 *src = static_cast<const BlockQ8 *>(blocks);
+    for (size_t b = 0; b < nb; b++) {
+        BlockQ8 blk;
+        std::memcpy(&blk, src + b, sizeof(blk));
+        const size_t slot = (b % nbr) * rows + b / nbr;
+        d[slot] = blk.d;
+        std::memcpy(&qs[slot * 32], blk.qs, 32);
+    }
+}
 }  // namespace
 
 extern "C" vh_status vh_q8_0_upload(const vh_runtime *rt, const void *blocks, size_t rows,
@@ -1301,18 +1409,10 @@ extern "C" vh_status vh_q8_0_upload(const vh_runtime *rt, const void *blocks, si
     GUARD_BEGIN
     RtState &s = *rt->s;
     TRY(set_device(s));
-    // AoS block (row r, k-slice j) -> block-major slot j * rows + r.
-    const size_t nb = n / 32, nbr = k / 32;
-    std::vector<int8_t> qs(n);
-    std::vector<uint16_t> d(nb);
-    const BlockQ8 *src = static_cast<const BlockQ8 *>(blocks);
-    for (size_t b = 0; b < nb; b++) {
-        BlockQ8 blk;
-        std::memcpy(&blk, src + b, sizeof(blk));
-        const size_t slot = (b % nbr) * rows + b / nbr;
-        d[slot] = blk.d;
-        std::memcpy(&qs[slot * 32], blk.qs, 32);
-    }
+    const size_t nb = n / 32;
+    std::vector<int8_t> qs;
+    std::vector<uint16_t> d;
+    unpack_q8_aos(blocks, rows, k, qs, d);
     vh_q8_tensor *t = nullptr;
     TRY(new_q8(rt->s, rows, k, &t));
     vh_status st = h2d(s, t->qs, qs.data(), n, "Q8_0 upload");
@@ -1420,6 +1520,119 @@ extern "C" vh_status vh_gemm_q8_0(const vh_runtime *rt, const vh_q8_tensor *a_q,
     GUARD_END
 }
 
+// ---- Q8_0 projection --------------------------------------------------------
+
+extern "C" vh_status vh_prepare_linear_q8_0(const vh_runtime *rt, size_t input_features,
+                                            size_t output_features, const void *weight_blocks,
+                                            const float *bias, const float *gamma,
+                                            vh_linear_q8 **out) {
+    NEED(rt, "vh_prepare_linear_q8_0");
+    NEED(out, "vh_prepare_linear_q8_0");
+    size_t kn = 0;
+    if (input_features % 32 != 0)
+        return fail(VH_ERR_KERNEL, "vh_prepare_linear_q8_0: input_features must be a multiple of "
+                                   "QK8_0, got " + std::to_string(input_features));
+    if (mul_overflows(input_features, output_features, &kn) || (kn && !weight_blocks))
+        return fail(VH_ERR_BLAS, "linear parameter shape K=" + std::to_string(input_features) +
+                                     ", N=" + std::to_string(output_features) +
+                                     " does not match the provided buffers");
+    if (input_features > INT32_MAX || output_features > INT32_MAX)
+        return fail(VH_ERR_BLAS, "linear dimension exceeds 2^31-1");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    std::vector<int8_t> qs;
+    std::vector<uint16_t> d;
+    unpack_q8_aos(weight_blocks, output_features, input_features, qs, d);
+    vh_linear_q8 *l = new vh_linear_q8;
+    l->rt = rt->s;
+    Q8Lin &L = l->L;
+    vh_status st = dalloc(s, kn, &L.qs, "Q8_0 weight allocation");
+    if (!st) st = dalloc(s, kn / 32, &L.d, "Q8_0 weight allocation");
+    if (!st) st = h2d(s, L.qs, qs.data(), kn, "Q8_0 weight upload");
+    if (!st) st = h2d(s, L.d, d.data(), kn / 32 * sizeof(uint16_t), "Q8_0 weight upload");
+    if (!st && bias) st = upload_array(s, bias, output_features, &L.bias, "linear bias upload");
+    if (!st && gamma) st = upload_array(s, gamma, output_features, &L.gamma, "linear gamma upload");
+    if (st) {
+        delete l;
+        return st;
+    }
+    L.K = input_features;
+    L.N = output_features;
+    *out = l;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" void vh_linear_q8_0_free(vh_linear_q8 *linear) { delete linear; }
+extern "C" size_t vh_linear_q8_0_input_features(const vh_linear_q8 *linear) {
+    return linear ? linear->L.K : 0;
+}
+extern "C" size_t vh_linear_q8_0_output_features(const vh_linear_q8 *linear) {
+    return linear ? linear->L.N : 0;
+}
+
+static vh_status check_q8_input(const vh_linear_q8 *linear, const vh_tensor *input, size_t rows,
+                                const char *name) {
+    NEED(linear, name);
+    NEED(input, name);
+    size_t expected = 0;
+    if (mul_overflows(rows, linear->L.K, &expected) || input->len != expected)
+        return fail(VH_ERR_BLAS, "linear input rows=" + std::to_string(rows) + ", K=" +
+                                     std::to_string(linear->L.K) +
+                                     " does not match device input length " +
+                                     std::to_string(input->len));
+    if (rows > INT32_MAX) return fail(VH_ERR_BLAS, "linear rows exceed 2^31-1");
+    return VH_OK;
+}
+
+static vh_status q8_linear_new(const vh_linear_q8 *linear, const vh_tensor *input, size_t rows,
+                               vh::Epi epi, const char *name, vh_tensor **out) {
+    TRY(check_q8_input(linear, input, rows, name));
+    NEED(out, name);
+    if (epi == vh::Epi::Gelu && linear->L.gamma)
+        return fail(VH_ERR_BLAS, std::string(name) + ": the linear carries a LayerScale gamma");
+    GUARD_BEGIN
+    RtState &s = *linear->rt;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(linear->rt, rows * linear->L.N, &t, "GEMM output allocation"));
+    vh_status st = rows ? run_q8(s, linear->L, input->ptr, rows, epi, t->ptr, name) : VH_OK;
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_linear_q8_0_run(const vh_linear_q8 *linear, const vh_tensor *input,
+                                        size_t rows, vh_tensor **out) {
+    return q8_linear_new(linear, input, rows, vh::Epi::Store, "gemm_q8_0_bias_scale", out);
+}
+
+extern "C" vh_status vh_linear_q8_0_run_gelu(const vh_linear_q8 *linear, const vh_tensor *input,
+                                             size_t rows, vh_tensor **out) {
+    return q8_linear_new(linear, input, rows, vh::Epi::Gelu, "gemm_q8_0_bias_gelu", out);
+}
+
+extern "C" vh_status vh_linear_q8_0_run_residual(const vh_linear_q8 *linear,
+                                                 const vh_tensor *input, size_t rows,
+                                                 vh_tensor *residual) {
+    TRY(check_q8_input(linear, input, rows, "vh_linear_q8_0_run_residual"));
+    NEED(residual, "vh_linear_q8_0_run_residual");
+    if (residual->len != rows * linear->L.N)
+        return mismatch(residual->len, rows * linear->L.N, "vh_linear_q8_0_run_residual");
+    GUARD_BEGIN
+    RtState &s = *linear->rt;
+    TRY(set_device(s));
+    if (rows == 0) return VH_OK;
+    return run_q8(s, linear->L, input->ptr, rows, vh::Epi::Residual, residual->ptr,
+                  "gemm_q8_0_bias_scale_residual");
+    GUARD_END
+}
+
 // =============================================================================
 // DA3-BASE encoder block
 // =============================================================================
@@ -1435,7 +1648,8 @@ vh_status upload_small(RtState &s, const float *h, size_t n, float **out, const 
 // One pre-norm block, in place on x.  With h_ready the caller has already
 // written LayerNorm1(x) into the block workspace (the previous block's fc2
 // fused it); with next, this block's fc2 writes the next block's
-// LayerNorm1(x) there the same way.
+// LayerNorm1(x) there the same way (f32 blocks only: a Q8_0 block ignores
+// next).
 vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size_t tokens,
                     const int64_t *pos, float freq, float eps, bool h_ready = false,
                     const vh_block *next = nullptr) {
@@ -1458,6 +1672,37 @@ vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size
         TRY(launch(s, "layernorm", [&] {
             return vh::launch_layernorm(s.stream, x, b.ln1_g, b.ln1_b, h, M, D, eps);
         }));
+    if (b.q8) {
+        // Q8_0 projections: each GEMM quantises its input rows first, so no
+        // LayerNorm rides in a GEMM epilogue and fc2 leaves the next block's
+        // LayerNorm1 to that block.
+        TRY(run_q8(s, b.qqkv, h, M, vh::Epi::Store, f, "gemm_q8_0_qkv"));
+        for (size_t i = 0; i < images; i++) {
+            const size_t o = i * tokens * D;
+            TRY(launch(s, "split_qkv", [&] {
+                return vh::launch_split_qkv(s.stream, f + 3 * o, q + o, k + o, v + o, tokens,
+                                            kHeads, 64);
+            }));
+        }
+        if (b.qn_g) {
+            TRY(launch(s, "qk_norm_rope", [&] {
+                return vh::launch_qk_norm_rope(s.stream, q, k, b.qn_g, b.qn_b, b.kn_g, b.kn_b,
+                                               rot, M * kHeads, tokens, eps);
+            }));
+        } else if (rot) {
+            for (float *t : {q, k})
+                TRY(launch(s, "rope2d", [&] {
+                    return vh::launch_rope2d(s.stream, t, images * kHeads, tokens, 64, rot);
+                }));
+        }
+        TRY(flash(s, q, k, v, att, images * kHeads, tokens, kHeads, true));
+        TRY(run_q8(s, b.qproj, att, M, vh::Epi::Residual, x, "gemm_q8_0_proj_residual"));
+        TRY(launch(s, "layernorm", [&] {
+            return vh::launch_layernorm(s.stream, x, b.ln2_g, b.ln2_b, h, M, D, eps);
+        }));
+        TRY(run_q8(s, b.qfc1, h, M, vh::Epi::Gelu, f, "gemm_q8_0_fc1_gelu"));
+        return run_q8(s, b.qfc2, f, M, vh::Epi::Residual, x, "gemm_q8_0_fc2_residual");
+    }
     if (b.qn_g) {
         // Late block: QKV with bias only, then LayerNorm of every 64-wide Q
         // and K head row fused with the RoPE (src/specialized.rs:278-316).
@@ -1490,8 +1735,8 @@ vh_status check_block_x(const vh_tensor *x, size_t images, size_t tokens) {
 }
 }  // namespace
 
-extern "C" vh_status vh_block_prepare(const vh_runtime *rt, const vh_block_params *p,
-                                      vh_block **out) {
+static vh_status block_prepare(const vh_runtime *rt, const vh_block_params *p, bool q8,
+                               vh_block **out) {
     NEED(rt, "vh_block_prepare");
     NEED(p, "vh_block_prepare");
     NEED(out, "vh_block_prepare");
@@ -1509,10 +1754,19 @@ extern "C" vh_status vh_block_prepare(const vh_runtime *rt, const vh_block_param
     TRY(set_device(s));
     vh_block *b = new vh_block;
     b->rt = rt->s;
-    vh_status st = prepare_lin(s, kDim, 3 * kDim, p->w_qkv, p->b_qkv, nullptr, &b->qkv);
-    if (!st) st = prepare_lin(s, kDim, kDim, p->w_proj, p->b_proj, p->ls1, &b->proj);
-    if (!st) st = prepare_lin(s, kDim, kMlp, p->w_fc1, p->b_fc1, nullptr, &b->fc1);
-    if (!st) st = prepare_lin(s, kMlp, kDim, p->w_fc2, p->b_fc2, p->ls2, &b->fc2);
+    b->q8 = q8;
+    vh_status st;
+    if (q8) {
+        st = prepare_q8_from_f32(s, kDim, 3 * kDim, p->w_qkv, p->b_qkv, nullptr, &b->qqkv);
+        if (!st) st = prepare_q8_from_f32(s, kDim, kDim, p->w_proj, p->b_proj, p->ls1, &b->qproj);
+        if (!st) st = prepare_q8_from_f32(s, kDim, kMlp, p->w_fc1, p->b_fc1, nullptr, &b->qfc1);
+        if (!st) st = prepare_q8_from_f32(s, kMlp, kDim, p->w_fc2, p->b_fc2, p->ls2, &b->qfc2);
+    } else {
+        st = prepare_lin(s, kDim, 3 * kDim, p->w_qkv, p->b_qkv, nullptr, &b->qkv);
+        if (!st) st = prepare_lin(s, kDim, kDim, p->w_proj, p->b_proj, p->ls1, &b->proj);
+        if (!st) st = prepare_lin(s, kDim, kMlp, p->w_fc1, p->b_fc1, nullptr, &b->fc1);
+        if (!st) st = prepare_lin(s, kMlp, kDim, p->w_fc2, p->b_fc2, p->ls2, &b->fc2);
+    }
     if (!st) st = upload_small(s, p->ln1_gamma, kDim, &b->ln1_g, "ln1 gamma");
     if (!st) st = upload_small(s, p->ln1_beta, kDim, &b->ln1_b, "ln1 beta");
     if (!st) st = upload_small(s, p->ln2_gamma, kDim, &b->ln2_g, "ln2 gamma");
@@ -1531,6 +1785,18 @@ extern "C" vh_status vh_block_prepare(const vh_runtime *rt, const vh_block_param
     return VH_OK;
     GUARD_END
 }
+
+extern "C" vh_status vh_block_prepare(const vh_runtime *rt, const vh_block_params *p,
+                                      vh_block **out) {
+    return block_prepare(rt, p, false, out);
+}
+
+extern "C" vh_status vh_block_prepare_q8_0(const vh_runtime *rt, const vh_block_params *p,
+                                           vh_block **out) {
+    return block_prepare(rt, p, true, out);
+}
+
+extern "C" int vh_block_is_q8_0(const vh_block *block) { return block && block->q8; }
 
 extern "C" void vh_block_free(vh_block *block) { delete block; }
 
@@ -1562,9 +1828,11 @@ extern "C" vh_status vh_encoder_run(const vh_runtime *rt, const vh_block *const 
     RtState &s = *rt->s;
     TRY(set_device(s));
     if (images * tokens == 0) return VH_OK;
+    // An f32 block's fc2 writes the next block's LayerNorm1; a Q8_0 block's
+    // does not, so the block after it normalises its own input.
     for (size_t i = 0; i < layers; i++)
         TRY(block_run(s, *blocks[i], x->ptr, images, tokens, pos_yx, rope_frequency, epsilon,
-                      i > 0, i + 1 < layers ? blocks[i + 1] : nullptr));
+                      i > 0 && !blocks[i - 1]->q8, i + 1 < layers ? blocks[i + 1] : nullptr));
     return VH_OK;
     GUARD_END
 }

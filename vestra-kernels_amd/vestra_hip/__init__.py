@@ -129,7 +129,16 @@ SIGNATURES = [
     ("vh_q8_tensor_k", _sz, [_p]),
     ("vh_quantize_q8_0", _S, [_p, _p, _sz, _sz, _pp]),
     ("vh_gemm_q8_0", _S, [_p, _p, _p, _sz, _sz, _sz, _pp]),
+    ("vh_prepare_linear_q8_0", _S, [_p, _sz, _sz, _p, _f32p, _f32p, _pp]),
+    ("vh_linear_q8_0_free", None, [_p]),
+    ("vh_linear_q8_0_input_features", _sz, [_p]),
+    ("vh_linear_q8_0_output_features", _sz, [_p]),
+    ("vh_linear_q8_0_run", _S, [_p, _p, _sz, _pp]),
+    ("vh_linear_q8_0_run_gelu", _S, [_p, _p, _sz, _pp]),
+    ("vh_linear_q8_0_run_residual", _S, [_p, _p, _sz, _p]),
     ("vh_block_prepare", _S, [_p, _p, _pp]),
+    ("vh_block_prepare_q8_0", _S, [_p, _p, _pp]),
+    ("vh_block_is_q8_0", ctypes.c_int, [_p]),
     ("vh_block_free", None, [_p]),
     ("vh_vit_block_run", _S, [_p, _p, _p, _sz, _sz, _i64p, ctypes.c_float, ctypes.c_float]),
     ("vh_encoder_run", _S, [_p, _pp, _sz, _p, _sz, _sz, _i64p, ctypes.c_float,
@@ -298,6 +307,42 @@ class Q8Tensor:
             pass
 
 
+class LinearQ8:
+    """A projection with BlockQ8_0 weights; input rows are quantised per run."""
+
+    def __init__(self, runtime: "Runtime", handle: int):
+        self._rt = runtime
+        self._h = ctypes.c_void_p(handle)
+
+    def input_features(self) -> int:
+        return int(lib().vh_linear_q8_0_input_features(self._h))
+
+    def output_features(self) -> int:
+        return int(lib().vh_linear_q8_0_output_features(self._h))
+
+    def _new(self, fn, x: Tensor, rows: int) -> Tensor:
+        out = ctypes.c_void_p()
+        _check(fn(self._h, x.handle, rows, ctypes.byref(out)))
+        return Tensor(self._rt, out.value)
+
+    def run(self, x: Tensor, rows: int) -> Tensor:
+        return self._new(lib().vh_linear_q8_0_run, x, rows)
+
+    def run_gelu(self, x: Tensor, rows: int) -> Tensor:
+        return self._new(lib().vh_linear_q8_0_run_gelu, x, rows)
+
+    def run_residual(self, x: Tensor, rows: int, residual: Tensor) -> None:
+        _check(lib().vh_linear_q8_0_run_residual(self._h, x.handle, rows, residual.handle))
+
+    def __del__(self):
+        try:
+            if self._h and self._h.value:
+                lib().vh_linear_q8_0_free(self._h)
+                self._h = ctypes.c_void_p(None)
+        except Exception:
+            pass
+
+
 class BlockParams(ctypes.Structure):
     _fields_ = [(n, _f32p) for n in da3.BLOCK_FIELDS + da3.QK_NORM_FIELDS]
 
@@ -312,6 +357,10 @@ class Block:
     @property
     def handle(self):
         return self._h
+
+    @property
+    def is_q8_0(self) -> bool:
+        return bool(lib().vh_block_is_q8_0(self._h))
 
     def __del__(self):
         try:
@@ -480,13 +529,29 @@ class Runtime:
     def gemm_q8_0(self, a_q: Q8Tensor, b_q: Q8Tensor, m, n, k) -> Tensor:
         return self._out(lib().vh_gemm_q8_0, a_q.handle, b_q.handle, m, n, k)
 
+    def prepare_linear_q8_0(self, input_features, output_features, weight_blocks, bias=None,
+                            gamma=None) -> LinearQ8:
+        """weight_blocks: output_features x input_features/32 BlockQ8_0 rows (W^T)."""
+        wb = np.ascontiguousarray(weight_blocks, BLOCK_Q8_0)
+        b = None if bias is None else _f32(bias).reshape(-1)
+        g = None if gamma is None else _f32(gamma).reshape(-1)
+        out = ctypes.c_void_p()
+        _check(lib().vh_prepare_linear_q8_0(self._h, input_features, output_features,
+                                            wb.ctypes.data if wb.size else None,
+                                            _fp(b) if b is not None else None,
+                                            _fp(g) if g is not None else None,
+                                            ctypes.byref(out)))
+        return LinearQ8(self, out.value)
+
     # -- DA3 block / encoder
-    def prepare_block(self, weights: dict) -> Block:
+    def prepare_block(self, weights: dict, q8_0: bool = False) -> Block:
+        """q8_0=True quantises the four projection weights to Q8_0 on the device."""
         keep = {n: _f32(weights[n]).reshape(-1) for n in da3.BLOCK_FIELDS + da3.QK_NORM_FIELDS
                 if weights.get(n) is not None}
         params = BlockParams(**{n: _fp(a) for n, a in keep.items()})
         out = ctypes.c_void_p()
-        _check(lib().vh_block_prepare(self._h, ctypes.byref(params), ctypes.byref(out)))
+        fn = lib().vh_block_prepare_q8_0 if q8_0 else lib().vh_block_prepare
+        _check(fn(self._h, ctypes.byref(params), ctypes.byref(out)))
         return Block(self, out.value)
 
     def vit_block_run(self, block: Block, x: Tensor, images, tokens, pos_yx=None,
