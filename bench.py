@@ -42,6 +42,13 @@ FLOPS = {
     "gemm_fc2_residual": 2.0 * T * F * D,
     "flash_attention": 4.0 * H * T * T * HD,
 }
+# Q8_0 projections: int8 multiply-adds x 2 per launch.
+INT8_OPS = {
+    "gemm_q8_0_qkv": 2.0 * T * D * 3 * D,
+    "gemm_q8_0_proj_residual": 2.0 * T * D * D,
+    "gemm_q8_0_fc1_gelu": 2.0 * T * D * F,
+    "gemm_q8_0_fc2_residual": 2.0 * T * F * D,
+}
 # Algorithmic HBM bytes per launch of the bandwidth-bound kernels.
 BYTES = {"layernorm": 2.0 * T * D * 4 + 2 * D * 4}
 
@@ -68,13 +75,13 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def gpu_block(steps: int, warmup: int) -> dict:
+def gpu_block(steps: int, warmup: int, q8_0: bool = False) -> dict:
     import vestra_hip as vh
     from vestra_hip import da3, seeded
 
     rt = vh.Runtime(0)
     w = da3.block_weights(seed=3)
-    block = rt.prepare_block(w)
+    block = rt.prepare_block(w, q8_0=q8_0)
     x0 = seeded.normal(300, T * D)
     pos = da3.positions_yx(24, 36)
     x = rt.upload_f32(x0)
@@ -85,7 +92,7 @@ def gpu_block(steps: int, warmup: int) -> dict:
     for _ in range(steps):
         rt.vit_block_run(block, x, 1, T, pos)
     total_ms = rt.timer_stop()
-    log(f"timed {steps} blocks: {total_ms:.3f} ms")
+    log(f"timed {steps} {'Q8_0 ' if q8_0 else ''}blocks: {total_ms:.3f} ms")
 
     rt.profile_reset()
     rt.profile_enable(True)
@@ -101,12 +108,15 @@ def gpu_block(steps: int, warmup: int) -> dict:
         if name in FLOPS:
             tf = FLOPS[name] / (avg_us * 1e-6) / 1e12
             entry.update(tflops=round(tf, 2), frac_fp32_mfma=round(tf / PEAK_FP32_MFMA_TFLOPS, 4))
+        if name in INT8_OPS:
+            entry.update(top_s=round(INT8_OPS[name] / (avg_us * 1e-6) / 1e12, 2))
         if name in BYTES:
             gbs = BYTES[name] / (avg_us * 1e-6) / 1e9
             entry.update(gbs=round(gbs, 1), frac_hbm=round(gbs / PEAK_HBM_GBS, 4))
         kernels[name] = entry
         log(f"  {name:22s} x{per_block:.0f}/block avg {avg_us:9.2f} us " +
             (f"{entry.get('tflops', 0):7.2f} TF/s" if 'tflops' in entry else
+             f"{entry.get('top_s', 0):7.2f} TOP/s" if 'top_s' in entry else
              f"{entry.get('gbs', 0):7.1f} GB/s" if 'gbs' in entry else ""))
     return {"ms_per_step": total_ms / steps, "kernels": kernels}
 
@@ -240,6 +250,7 @@ def main() -> int:
 
     gpu = gpu_block(args.steps, args.warmup)
     q8 = gpu_q8_0(max(10, min(args.steps, 100)))
+    q8_block = gpu_block(max(10, min(args.steps, 100)), args.warmup, q8_0=True)
     elementwise = gpu_elementwise()
     if args.calibrate:
         import vestra_hip as vh
@@ -286,6 +297,9 @@ def main() -> int:
         },
         "kernels": ker,
         "q8_0": q8,
+        "q8_0_block": {"workload": "vit_block_865_q8_0_projections",
+                       "us_per_block": round(q8_block["ms_per_step"] * 1e3, 2),
+                       "kernels": q8_block["kernels"]},
         "elementwise_at_scale": elementwise,
     }
     if not args.no_cpu:

@@ -351,6 +351,22 @@ def test_quantize_q8_0_bit_exact(rt, rows, k):
     assert np.array_equal(got["qs"], exp["qs"])
 
 
+def test_q8_0_upload_download_every_int8_value(rt):
+    """Every int8 value (-128 included, as GGUF files may hold it) and
+    arbitrary scale bits survive the device's block-major repack."""
+    rows, k = 3, 256
+    blocks = np.zeros(rows * k // 32, vh.BLOCK_Q8_0)
+    blocks["qs"] = np.arange(rows * k, dtype=np.int64).reshape(-1, 32) % 256 - 128
+    blocks["d"] = np.arange(blocks.size, dtype=np.uint16) * 2477 + 1
+    got = rt.q8_0_download(rt.q8_0_upload(blocks, rows, k))
+    assert np.array_equal(got["qs"], blocks["qs"]) and np.array_equal(got["d"], blocks["d"])
+    # -128 operands: |isum| = 32 * 128^2 still exact
+    a = np.zeros(1, vh.BLOCK_Q8_0)
+    a["qs"], a["d"] = -128, 0x3C00  # d = 1.0
+    c = rt.download_f32(rt.gemm_q8_0(rt.q8_0_upload(a, 1, 32), rt.q8_0_upload(a, 1, 32), 1, 1, 32))
+    assert c[0] == 32 * 128 * 128
+
+
 @pytest.mark.parametrize("m,n,k", [(865, 3072, 768), (8, 8, 64), (5, 17, 96), (64, 96, 3072),
                                    (33, 70, 1056)])
 def test_gemm_q8_0_bit_exact(rt, m, n, k):

@@ -8,10 +8,15 @@
 // block is 512 contiguous bytes and a k-slice of scales is contiguous.
 //
 // GEMM: per 32-wide block b, one v_mfma_i32_16x16x32_i8 produces the exact
-// int32 sums isum_b of a 16x16 tile (|isum| <= 32*127*127 < 2^24, so the
+// int32 sums isum_b of a 16x16 tile (|isum| <= 32*128*128 < 2^24, so the
 // float conversion is exact).  Each lane then folds its four outputs in block
 // order exactly as src/scalar.rs:51 does: acc = acc + (d_a * d_b) * isum,
-// three separately rounded ops.
+// three separately rounded ops.  (Holding the int8 values as halves for the
+// f16 MFMA would drop the conversion, but doubles the operand bytes and
+// measured slower: the operands no longer stay in L2.)
+#include <cstdlib>
+#include <cstring>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -61,14 +66,17 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
     reinterpret_cast<uint32_t *>(qs + dst * 32)[part] = w;
 }
 
-// 256 threads = 4 waves in a 2x2 arrangement over a 64x64 output tile; each
-// wave owns 32x32 = 2x2 MFMA fragments.  The scales of a chunk of up to
-// QCH blocks are staged in LDS as floats, [block][row] and [block][col], so
-// a lane's four output rows (4*lh..4*lh+3 of a fragment) are one 16-byte
-// read.  The int8 operands stream from global memory (clamped rows, no
-// select) with a register prefetch PF blocks ahead.
-constexpr int QCH = 32;  // blocks per scale chunk (a multiple of QPF)
-constexpr int QPF = 4;   // prefetch distance in blocks
+// 256 threads = 4 waves in a 2x2 arrangement; each wave owns FM x FN MFMA
+// fragments of 16x16, so a workgroup covers (32*FM) x (32*FN) outputs (FM,
+// FN in {1, 2}: the small tiles give the narrow projections enough
+// workgroups, since the block-order fold cannot be split along K).  The
+// scales of a chunk of up to QCH blocks are staged in LDS as floats,
+// [block][row] and [block][col], so a lane's four output rows (4*lh..4*lh+3
+// of a fragment) are one 16-byte read.  The operands stream from global
+// memory (clamped rows, no select) with a register prefetch QPF blocks
+// ahead, and the MFMAs of block b+1 are issued before the fold of block b,
+// so the matrix core works while the VALU folds.
+constexpr int QCH = 32;  // blocks per scale chunk (a multiple of the prefetch distance)
 
 // Epilogue of a Q8_0 projection, applied to the exact block-order sum with
 // separately rounded ops (the f32 ops the engine applies after
@@ -78,118 +86,220 @@ constexpr int QPF = 4;   // prefetch distance in blocks
 struct Q8Epi {
     const float *bias, *gamma;
     size_t tail_start;
+    // Qkv: c is unused; columns [0, 3*heads*64) go to q / k / v head-major
+    // [img][head][token][64] with the bias added, and when rot is non-null the
+    // 2-D RoPE (rot [tokens][2][16][sin, cos]) rotates the q and k columns.
+    float *q, *k, *v;
+    const float *rot;
+    int tokens, heads;
 };
 
-template <Epi EPI>
+template <Epi EPI, int FM, int FN>
 __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict__ a_qs,
                                                         const uint16_t *__restrict__ a_d,
                                                         const int8_t *__restrict__ b_qs,
                                                         const uint16_t *__restrict__ b_d,
                                                         float *__restrict__ c, int M, int N,
                                                         int K, Q8Epi ep) {
-    __shared__ __attribute__((aligned(16))) float sa[QCH][64];
-    __shared__ __attribute__((aligned(16))) float sb[QCH][64];
+    static_assert(EPI != Epi::Qkv || FN == 2, "the QKV epilogue pairs fragments j = 0, 1");
+    constexpr int TR = 32 * FM, TC = 32 * FN;  // workgroup tile
+    constexpr int QPF = 4;  // prefetch distance in blocks
+    __shared__ __attribute__((aligned(16))) float sa[QCH][TR];
+    __shared__ __attribute__((aligned(16))) float sb[QCH][TC];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lh = lane >> 4;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-    const int mw = m0 + wm * 32;
-    const int nw = n0 + wn * 32;
+    const int m0 = blockIdx.y * TR, n0 = blockIdx.x * TC;
+    const int mw = m0 + wm * 16 * FM;
+    const int nw = n0 + wn * 16 * FN;
     const int nb = K / 32;
 
     // Operand rows of this lane (clamped: rows past M / N compute values
-    // that are never stored); block b of row r sits at (b * rows + r) * 32.
-    const int8_t *arow[2], *brow[2];
+    // that are never stored); block b of row r sits at byte (b * rows + r) *
+    // 32.  Buffer loads take the per-lane row offset in a VGPR and the
+    // block's offset b * rows * 32 in an SGPR, so a block costs no vector
+    // address arithmetic.  The host keeps rows * K below 2^31.
+    const __amdgpu_buffer_rsrc_t rsa =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a_qs, (short)0, M * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)b_qs, (short)0, N * K, 0x00020000);
+    int aoff[FM], boff[FN];
 #pragma unroll
-    for (int i = 0; i < 2; i++) arow[i] = a_qs + (size_t)min(mw + i * 16 + li, M - 1) * 32 + 8 * lh;
+    for (int i = 0; i < FM; i++) aoff[i] = min(mw + i * 16 + li, M - 1) * 32 + 8 * lh;
 #pragma unroll
-    for (int j = 0; j < 2; j++) brow[j] = b_qs + (size_t)min(nw + j * 16 + li, N - 1) * 32 + 8 * lh;
+    for (int j = 0; j < FN; j++) boff[j] = min(nw + j * 16 + li, N - 1) * 32 + 8 * lh;
 
-    f32x4 acc[2][2];
+    f32x4 acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < FN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    long pa[QPF][2], pb[QPF][2];
+    long pa[QPF][FM], pb[QPF][FN];
     auto fetch = [&](int b, int slot) {
         const int bc = min(b, nb - 1);
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-            pa[slot][i] = *reinterpret_cast<const long *>(arow[i] + (size_t)bc * M * 32);
+        for (int i = 0; i < FM; i++)
+            pa[slot][i] = __builtin_bit_cast(
+                long, __builtin_amdgcn_raw_buffer_load_b64(rsa, aoff[i], bc * M * 32, 0));
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-            pb[slot][j] = *reinterpret_cast<const long *>(brow[j] + (size_t)bc * N * 32);
+        for (int j = 0; j < FN; j++)
+            pb[slot][j] = __builtin_bit_cast(
+                long, __builtin_amdgcn_raw_buffer_load_b64(rsb, boff[j], bc * N * 32, 0));
     };
+    // Exact int32 block sums of the block held in prefetch slot `slot`.
+    auto block_sums = [&](int slot, i32x4 (&is)[FM][FN]) {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+                is[i][j] = mfma16x16x32_i8(pa[slot][i], pb[slot][j], i32x4{0, 0, 0, 0});
+    };
+    // Scales of one chunk, NA + NB per thread, loaded into registers a chunk
+    // ahead (all loads issued before any is waited on) and stored to LDS
+    // when the chunk starts.  Indices are clamped; stores past the chunk's
+    // last block are skipped.
+    constexpr int NA = TR * QCH / 256, NB = TC * QCH / 256;
+    uint16_t ra[NA], rb[NB];
+    auto load_scales = [&](int c) {
+        const int last = min(QCH, nb - c) - 1;
+#pragma unroll
+        for (int t = 0; t < NA; t++) {
+            const int e = tid + 256 * t, blk = min(e / TR, last);
+            ra[t] = a_d[(size_t)(c + blk) * M + min(m0 + e % TR, M - 1)];
+        }
+#pragma unroll
+        for (int t = 0; t < NB; t++) {
+            const int e = tid + 256 * t, blk = min(e / TC, last);
+            rb[t] = b_d[(size_t)(c + blk) * N + min(n0 + e % TC, N - 1)];
+        }
+    };
+    i32x4 cur[FM][FN];
     if (nb > 0) {  // K == 0 stores zeros
+        load_scales(0);
 #pragma unroll
         for (int p = 0; p < QPF; p++) fetch(p, p);
+        block_sums(0, cur);
+        fetch(QPF, 0);
     }
 
     for (int c0 = 0; c0 < nb; c0 += QCH) {
         const int cn = min(QCH, nb - c0);
         __syncthreads();  // previous chunk's scales are no longer read
-        for (int e = tid; e < 64 * cn; e += 256) {
-            const int blk = e / 64, rr = e % 64;
-            sa[blk][rr] = half_bits_to_float(a_d[(size_t)(c0 + blk) * M + min(m0 + rr, M - 1)]);
-            sb[blk][rr] = half_bits_to_float(b_d[(size_t)(c0 + blk) * N + min(n0 + rr, N - 1)]);
+#pragma unroll
+        for (int t = 0; t < NA; t++) {
+            const int e = tid + 256 * t;
+            if (e / TR < cn) sa[e / TR][e % TR] = half_bits_to_float(ra[t]);
+        }
+#pragma unroll
+        for (int t = 0; t < NB; t++) {
+            const int e = tid + 256 * t;
+            if (e / TC < cn) sb[e / TC][e % TC] = half_bits_to_float(rb[t]);
         }
         __syncthreads();
-        // Groups of QPF blocks with the prefetch slot fixed at compile time
+        if (c0 + QCH < nb) load_scales(c0 + QCH);
+        // Groups of QPF blocks with the prefetch slots fixed at compile time
         // (QCH is a multiple of QPF, so block c0 + bl + u sits in slot u).
         for (int bl = 0; bl < cn; bl += QPF) {
 #pragma unroll
             for (int u = 0; u < QPF; u++) {
                 if (bl + u >= cn) break;
                 const int b = c0 + bl + u;
-                const long av[2] = {pa[u][0], pa[u][1]}, bv[2] = {pb[u][0], pb[u][1]};
-                fetch(b + QPF, u);
-                f32x4 da[2];
+                // Block b+1 (slot (u+1) % QPF) goes to the matrix core first;
+                // past the last block it recomputes a clamped block, unused.
+                i32x4 nxt[FM][FN];
+                block_sums((u + 1) % QPF, nxt);
+                fetch(b + 1 + QPF, (u + 1) % QPF);
+                f32x4 da[FM];
 #pragma unroll
-                for (int i = 0; i < 2; i++)
-                    da[i] = *reinterpret_cast<const f32x4 *>(&sa[bl + u][wm * 32 + i * 16 + 4 * lh]);
-                float db[2];
+                for (int i = 0; i < FM; i++)
+                    da[i] = *reinterpret_cast<const f32x4 *>(&sa[bl + u][wm * 16 * FM + i * 16 + 4 * lh]);
+                float db[FN];
 #pragma unroll
-                for (int j = 0; j < 2; j++) db[j] = sb[bl + u][wn * 32 + j * 16 + li];
-                i32x4 is[2][2];
+                for (int j = 0; j < FN; j++) db[j] = sb[bl + u][wn * 16 * FN + j * 16 + li];
 #pragma unroll
-                for (int i = 0; i < 2; i++)
+                for (int i = 0; i < FM; i++)
 #pragma unroll
-                    for (int j = 0; j < 2; j++) is[i][j] = mfma16x16x32_i8(av[i], bv[j], i32x4{0, 0, 0, 0});
-#pragma unroll
-                for (int i = 0; i < 2; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
+                    for (int j = 0; j < FN; j++)
 #pragma unroll
                         for (int r = 0; r < 4; r++)
                             acc[i][j][r] = add_rn(acc[i][j][r],
-                                                  mul_rn(mul_rn(da[i][r], db[j]), (float)is[i][j][r]));
+                                                  mul_rn(mul_rn(da[i][r], db[j]), (float)cur[i][j][r]));
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++) cur[i][j] = nxt[i][j];
             }
         }
     }
     // Epilogue reads (bias, gamma, residual) from clamped indices before any
     // store, so that they overlap.
-    float bias[2], gamma[2], resid[2][2][4];
+    float bias[FN], gamma[FN], resid[FM][FN][4];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < FN; j++) {
         const int col = min(nw + j * 16 + li, N - 1);
         bias[j] = ep.bias ? ep.bias[col] : 0.0f;
         gamma[j] = ep.gamma ? ep.gamma[col] : 1.0f;
     }
     if constexpr (EPI == Epi::Residual) {
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < FM; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int j = 0; j < FN; j++)
 #pragma unroll
                 for (int r = 0; r < 4; r++)
                     resid[i][j][r] = c[(size_t)min(mw + i * 16 + 4 * lh + r, M - 1) * N +
                                        min(nw + j * 16 + li, N - 1)];
     }
+    if constexpr (EPI == Epi::Qkv) {
+        // The wave's 32 columns are one axis half of one head (N is a
+        // multiple of 64): fragment j = 0 holds dims d0 + li, j = 1 holds
+        // d0 + 16 + li, the (i, i + 16) pairs of rope::rotate_half
+        // (src/rope.rs:84-93).
+        if (nw >= N) return;
+        const int per = ep.heads * 64;
+        const int group = nw / per, head = (nw % per) / 64, d0 = nw % 64;
+        float *dst = group == 0 ? ep.q : (group == 1 ? ep.k : ep.v);
+        const bool rope = ep.rot != nullptr && group < 2;
+        float2 rot[FM][4];
+        if (rope) {
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+            for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+                for (int r = 0; r < 4; r++) {
+                    const int t = min(mw + i * 16 + 4 * lh + r, M - 1) % ep.tokens;
+                    rot[i][r] = *reinterpret_cast<const float2 *>(
+                        ep.rot + (((size_t)t * 2 + d0 / 32) * 16 + li) * 2);
+                }
+        }
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int row = mw + i * 16 + 4 * lh + r;
+                if (row >= M) continue;
+                const int img = row / ep.tokens, t = row % ep.tokens;
+                float a = acc[i][0][r], b = acc[i][1][r];
+                if (ep.bias) {
+                    a = add_rn(a, bias[0]);
+                    b = add_rn(b, bias[1]);
+                }
+                if (rope) {
+                    const float sn = rot[i][r].x, cs = rot[i][r].y;
+                    const float ra = sub_rn(mul_rn(a, cs), mul_rn(b, sn));
+                    b = add_rn(mul_rn(b, cs), mul_rn(a, sn));
+                    a = ra;
+                }
+                float *orow = dst + (((size_t)img * ep.heads + head) * ep.tokens + t) * 64 + d0;
+                orow[li] = a;
+                orow[16 + li] = b;
+            }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
             const int col = nw + j * 16 + li;
             if (col >= N) continue;
 #pragma unroll
@@ -220,19 +330,84 @@ hipError_t launch_quantize_q8_0(hipStream_t s, const float *x, int8_t *qs, uint1
     return hipGetLastError();
 }
 
+// Workgroup tile (FM, FN) of a Q8_0 GEMM: 64x64 when the grid has enough
+// workgroups for the 256 CUs, else 32x32 (VESTRA_HIP_Q8_TILE=2x2|2x1|1x2|1x1
+// overrides).
+static void q8_tile(size_t m, size_t n, int *fm, int *fn) {
+    static const char *env = std::getenv("VESTRA_HIP_Q8_TILE");
+    if (env && std::strlen(env) == 3 && (env[0] == '1' || env[0] == '2') && env[1] == 'x' &&
+        (env[2] == '1' || env[2] == '2')) {
+        *fm = env[0] - '0';
+        *fn = env[2] - '0';
+        return;
+    }
+    const size_t tiles64 = ((m + 63) / 64) * ((n + 63) / 64);
+    *fm = *fn = tiles64 >= 480 ? 2 : 1;
+}
+
+template <Epi EPI, int FM, int FN>
+static void q8_launch(hipStream_t s, const int8_t *a_qs, const uint16_t *a_d, const int8_t *b_qs,
+                      const uint16_t *b_d, float *c, size_t m, size_t n, size_t k,
+                      const Q8Epi &ep) {
+    dim3 grid((unsigned)((n + 32 * FN - 1) / (32 * FN)), (unsigned)((m + 32 * FM - 1) / (32 * FM)));
+    gemm_q8_0_kernel<EPI, FM, FN><<<grid, 256, 0, s>>>(a_qs, a_d, b_qs, b_d, c, (int)m, (int)n,
+                                                       (int)k, ep);
+}
+
+template <Epi EPI>
+static void q8_dispatch(hipStream_t s, const int8_t *a_qs, const uint16_t *a_d,
+                        const int8_t *b_qs, const uint16_t *b_d, float *c, size_t m, size_t n,
+                        size_t k, const Q8Epi &ep) {
+    int fm, fn;
+    q8_tile(m, n, &fm, &fn);
+    if (fm == 2 && fn == 2) q8_launch<EPI, 2, 2>(s, a_qs, a_d, b_qs, b_d, c, m, n, k, ep);
+    else if (fm == 2) q8_launch<EPI, 2, 1>(s, a_qs, a_d, b_qs, b_d, c, m, n, k, ep);
+    else if (fn == 2) q8_launch<EPI, 1, 2>(s, a_qs, a_d, b_qs, b_d, c, m, n, k, ep);
+    else q8_launch<EPI, 1, 1>(s, a_qs, a_d, b_qs, b_d, c, m, n, k, ep);
+}
+
+// The kernel addresses each operand with 32-bit buffer offsets.
+static bool q8_operands_fit(size_t m, size_t n, size_t k) {
+    return m * k <= (size_t)INT32_MAX && n * k <= (size_t)INT32_MAX;
+}
+
 hipError_t launch_gemm_q8_0(hipStream_t s, const int8_t *a_qs, const uint16_t *a_d,
                             const int8_t *b_qs, const uint16_t *b_d, float *c, size_t m,
                             size_t n, size_t k, Epi epi, const float *bias, const float *gamma) {
     if (m == 0 || n == 0) return hipSuccess;
-    dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64));
-    const Q8Epi ep{bias, gamma, m * n - (m * n) % 16};
-    const int M = (int)m, N = (int)n, K = (int)k;
+    if (!q8_operands_fit(m, n, k)) return hipErrorInvalidValue;
+    Q8Epi ep{};
+    ep.bias = bias;
+    ep.gamma = gamma;
+    ep.tail_start = m * n - (m * n) % 16;
     switch (epi) {
-        case Epi::Store: gemm_q8_0_kernel<Epi::Store><<<grid, 256, 0, s>>>(a_qs, a_d, b_qs, b_d, c, M, N, K, ep); break;
-        case Epi::Gelu: gemm_q8_0_kernel<Epi::Gelu><<<grid, 256, 0, s>>>(a_qs, a_d, b_qs, b_d, c, M, N, K, ep); break;
-        case Epi::Residual: gemm_q8_0_kernel<Epi::Residual><<<grid, 256, 0, s>>>(a_qs, a_d, b_qs, b_d, c, M, N, K, ep); break;
+        case Epi::Store: q8_dispatch<Epi::Store>(s, a_qs, a_d, b_qs, b_d, c, m, n, k, ep); break;
+        case Epi::Gelu: q8_dispatch<Epi::Gelu>(s, a_qs, a_d, b_qs, b_d, c, m, n, k, ep); break;
+        case Epi::Residual: q8_dispatch<Epi::Residual>(s, a_qs, a_d, b_qs, b_d, c, m, n, k, ep); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_q8_0_qkv(hipStream_t s, const int8_t *a_qs, const uint16_t *a_d,
+                                const int8_t *b_qs, const uint16_t *b_d, size_t m, size_t k,
+                                const float *bias, float *q, float *kk, float *v, size_t tokens,
+                                size_t heads, const float *rot) {
+    const size_t n = 3 * heads * 64;
+    if (m == 0 || heads == 0) return hipSuccess;
+    if (tokens == 0 || m % tokens != 0 || !q8_operands_fit(m, n, k)) return hipErrorInvalidValue;
+    Q8Epi ep{};
+    ep.bias = bias;
+    ep.q = q;
+    ep.k = kk;
+    ep.v = v;
+    ep.rot = rot;
+    ep.tokens = (int)tokens;
+    ep.heads = (int)heads;
+    int fm, fn;
+    q8_tile(m, n, &fm, &fn);
+    if (fm == 2) q8_launch<Epi::Qkv, 2, 2>(s, a_qs, a_d, b_qs, b_d, nullptr, m, n, k, ep);
+    else q8_launch<Epi::Qkv, 1, 2>(s, a_qs, a_d, b_qs, b_d, nullptr, m, n, k, ep);
     return hipGetLastError();
 }
 

@@ -95,5 +95,12 @@ hipError_t launch_gemm_q8_0(hipStream_t s, const int8_t *a_qs, const uint16_t *a
                             const int8_t *b_qs, const uint16_t *b_d, float *c, size_t m,
                             size_t n, size_t k, Epi epi = Epi::Store, const float *bias = nullptr,
                             const float *gamma = nullptr);
+// The QKV projection in Q8_0 (n = 3*heads*64): bias, then q/k/v head-major
+// [img][head][token][64] with the 2-D RoPE of q and k when rot is non-null
+// (rot [tokens][2][16][sin, cos]); m must be a multiple of tokens.
+hipError_t launch_gemm_q8_0_qkv(hipStream_t s, const int8_t *a_qs, const uint16_t *a_d,
+                                const int8_t *b_qs, const uint16_t *b_d, size_t m, size_t k,
+                                const float *bias, float *q, float *kk, float *v, size_t tokens,
+                                size_t heads, const float *rot);
 
 }  // namespace vh

@@ -490,6 +490,22 @@ vh_status run_q8(RtState &s, const Q8Lin &L, const float *in, size_t rows, vh::E
     });
 }
 
+// The QKV projection in Q8_0, written head-major with the RoPE when rot is set.
+vh_status run_q8_qkv(RtState &s, const Q8Lin &L, const float *in, size_t images, size_t tokens,
+                     const float *rot, float *q, float *k, float *v) {
+    const size_t rows = images * tokens;
+    int8_t *qs = nullptr;
+    uint16_t *d = nullptr;
+    TRY(q8_workspace(s, rows, L.K, &qs, &d));
+    TRY(launch(s, "quantize_q8_0", [&] {
+        return vh::launch_quantize_q8_0(s.stream, in, qs, d, rows, L.K);
+    }));
+    return launch(s, "gemm_q8_0_qkv", [&] {
+        return vh::launch_gemm_q8_0_qkv(s.stream, qs, d, L.qs, L.d, rows, L.K, L.bias, q, k, v,
+                                        tokens, L.N / 192, rot);
+    });
+}
+
 // f32 weights [K][N] row-major -> Q8_0 blocks of W^T rows, quantised on the
 // device with the activation kernel (quantize_row_q8_0 of each column).
 vh_status prepare_q8_from_f32(RtState &s, size_t K, size_t N, const float *w, const float *bias,
@@ -1676,24 +1692,14 @@ vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size
         // Q8_0 projections: each GEMM quantises its input rows first, so no
         // LayerNorm rides in a GEMM epilogue and fc2 leaves the next block's
         // LayerNorm1 to that block.
-        TRY(run_q8(s, b.qqkv, h, M, vh::Epi::Store, f, "gemm_q8_0_qkv"));
-        for (size_t i = 0; i < images; i++) {
-            const size_t o = i * tokens * D;
-            TRY(launch(s, "split_qkv", [&] {
-                return vh::launch_split_qkv(s.stream, f + 3 * o, q + o, k + o, v + o, tokens,
-                                            kHeads, 64);
-            }));
-        }
         if (b.qn_g) {
+            TRY(run_q8_qkv(s, b.qqkv, h, images, tokens, nullptr, q, k, v));
             TRY(launch(s, "qk_norm_rope", [&] {
                 return vh::launch_qk_norm_rope(s.stream, q, k, b.qn_g, b.qn_b, b.kn_g, b.kn_b,
                                                rot, M * kHeads, tokens, eps);
             }));
-        } else if (rot) {
-            for (float *t : {q, k})
-                TRY(launch(s, "rope2d", [&] {
-                    return vh::launch_rope2d(s.stream, t, images * kHeads, tokens, 64, rot);
-                }));
+        } else {
+            TRY(run_q8_qkv(s, b.qqkv, h, images, tokens, rot, q, k, v));
         }
         TRY(flash(s, q, k, v, att, images * kHeads, tokens, kHeads, true));
         TRY(run_q8(s, b.qproj, att, M, vh::Epi::Residual, x, "gemm_q8_0_proj_residual"));
