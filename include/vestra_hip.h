@@ -48,6 +48,8 @@ typedef struct vh_linear vh_linear;       /* CudaLinearF32 (src/cuda.rs:1291-129
 typedef struct vh_q8_tensor vh_q8_tensor; /* device rows of BlockQ8_0 (src/lib.rs:33-38) */
 typedef struct vh_block vh_block;         /* prepared DA3-BASE encoder block */
 typedef struct vh_linear_q8 vh_linear_q8; /* projection with BlockQ8_0 weights */
+typedef struct vh_conv2d vh_conv2d;       /* prepared 2-D convolution (DPT head) */
+typedef struct vh_conv_transpose2d vh_conv_transpose2d; /* prepared transposed convolution */
 
 /* ---- errors --------------------------------------------------------------- */
 /* Message of the calling thread's last failure ("" if none). */
@@ -289,6 +291,73 @@ vh_status vh_vit_block_run(const vh_runtime *rt, const vh_block *block, vh_tenso
 vh_status vh_encoder_run(const vh_runtime *rt, const vh_block *const *blocks, size_t layers,
                          vh_tensor *x, size_t images, size_t tokens, const int64_t *pos_yx,
                          float rope_frequency, float epsilon);
+
+/* ---- DPT head: convolution, transposed convolution, resize ----------------- */
+/* Batch-1 CHW tensors as in src/conv.rs and src/resample.rs.  Convolutions run
+ * as fp32-MFMA GEMMs (direct convolution: the crate's 3x3 stride-1 pad-1
+ * Winograd F(2x2,3x3) path is tested against the same direct definition,
+ * src/conv.rs:1438-1477); results agree with conv2d_naive (src/conv.rs:950-
+ * 998) within f32 accumulation error.  The resizes are bit-exact. */
+
+/* conv2d (src/conv.rs:877-945) with the weight prepared once, as
+ * prepare_winograd_f2_filter (src/conv.rs:174-177) prepares it for the CPU:
+ * weight OIHW [out_c*in_c*kh*kw], bias [out_c] or NULL. */
+vh_status vh_prepare_conv2d_f32(const vh_runtime *rt, size_t in_c, size_t out_c, size_t kh,
+                                size_t kw, size_t stride, size_t pad, const float *weight,
+                                const float *bias, vh_conv2d **out);
+void vh_conv2d_free(vh_conv2d *conv);
+/* oh = (ih + 2*pad - kh)/stride + 1 (0 when the kernel exceeds the padded input). */
+size_t vh_conv2d_output_height(const vh_conv2d *conv, size_t ih);
+size_t vh_conv2d_output_width(const vh_conv2d *conv, size_t iw);
+/* input [in_c*ih*iw] -> new [out_c*oh*ow] (conv3x3_winograd_f2_prepared,
+ * src/conv.rs:282-293, for any kernel, stride and padding). */
+vh_status vh_conv2d_run(const vh_conv2d *conv, const vh_tensor *input, size_t ih, size_t iw,
+                        vh_tensor **out);
+/* The same on max(input, 0) (conv3x3_winograd_f2_prepared_relu_input,
+ * src/conv.rs:651-679): the ReLU is applied while the patches are gathered. */
+vh_status vh_conv2d_run_relu_input(const vh_conv2d *conv, const vh_tensor *input, size_t ih,
+                                   size_t iw, vh_tensor **out);
+/* conv3x3_winograd_f2_prepared_resize_align_corners (src/conv.rs:304-320):
+ * align-corners resize of input [in_c*ih*iw] to oh x ow, plus add
+ * [in_c*oh*ow] when non-NULL, then the convolution. */
+vh_status vh_conv2d_run_resize_align_corners(const vh_conv2d *conv, const vh_tensor *input,
+                                             size_t ih, size_t iw, size_t oh, size_t ow,
+                                             const vh_tensor *add, vh_tensor **out);
+/* conv2d (src/conv.rs:877-945) in one call: host weight OIHW, bias or NULL. */
+vh_status vh_conv2d_f32(const vh_runtime *rt, const vh_tensor *input, size_t in_c, size_t ih,
+                        size_t iw, const float *weight, size_t out_c, size_t kh, size_t kw,
+                        size_t stride, size_t pad, const float *bias, vh_tensor **out);
+
+/* Transposed convolution (src/conv.rs:1009-1098), weight IOHW
+ * [in_c*out_c*kh*kw], bias [out_c] or NULL, oh = (ih-1)*stride + kh.  With
+ * kernel == stride (the DPT resize layers) the filter is packed as
+ * prepare_nonoverlap_transpose_filter does (src/conv.rs:83-93,
+ * src/specialized.rs:148-174) and the op is one GEMM plus a patch scatter;
+ * any other geometry gathers per output element in the order of the
+ * crate's conv_transpose2d_naive (src/conv.rs:1646-1704), bit-exact with it. */
+vh_status vh_prepare_conv_transpose2d_f32(const vh_runtime *rt, size_t in_c, size_t out_c,
+                                          size_t kh, size_t kw, size_t stride,
+                                          const float *weight, const float *bias,
+                                          vh_conv_transpose2d **out);
+void vh_conv_transpose2d_free(vh_conv_transpose2d *conv);
+/* conv_transpose2d_prepared (src/conv.rs:95-105): input [in_c*ih*iw], ih, iw >= 1. */
+vh_status vh_conv_transpose2d_run(const vh_conv_transpose2d *conv, const vh_tensor *input,
+                                  size_t ih, size_t iw, vh_tensor **out);
+/* conv_transpose2d (src/conv.rs:1009-1098) in one call. */
+vh_status vh_conv_transpose2d_f32(const vh_runtime *rt, const vh_tensor *input, size_t in_c,
+                                  size_t ih, size_t iw, const float *weight, size_t out_c,
+                                  size_t kh, size_t kw, size_t stride, const float *bias,
+                                  vh_tensor **out);
+
+/* bilinear_resize (src/resample.rs:10-77): half-pixel centres, clamp to edge;
+ * [c*ih*iw] -> new [c*oh*ow].  An empty input gives zeros. */
+vh_status vh_bilinear_resize_f32(const vh_runtime *rt, const vh_tensor *input, size_t c,
+                                 size_t ih, size_t iw, size_t oh, size_t ow, vh_tensor **out);
+/* bilinear_resize_align_corners (src/resample.rs:184-245), then + add
+ * [c*oh*ow] when add is non-NULL (the DPT UV-embedding add). */
+vh_status vh_bilinear_resize_align_corners_f32(const vh_runtime *rt, const vh_tensor *input,
+                                               size_t c, size_t ih, size_t iw, size_t oh,
+                                               size_t ow, const vh_tensor *add, vh_tensor **out);
 
 /* ---- profiling (device twin of DA3_FLASH_PROFILE, src/specialized.rs:1324) - */
 /* When enabled, every kernel launch is bracketed by HIP events on the

@@ -85,6 +85,13 @@ def _declare(L):
     sig("vko_qkv", None, _sz, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p)
     sig("vko_split_qkv_hnd", None, _f32p, _sz, _sz, _sz, _f32p, _f32p, _f32p)
     sig("vko_hnd_to_token", None, _f32p, _sz, _sz, _sz, _f32p)
+    sig("vko_conv2d_naive", None, _f32p, _sz, _sz, _sz, _f32p, _sz, _sz, _sz, _sz, _sz, _f32p,
+        _f32p)
+    for name in ("vko_conv_transpose2d", "vko_conv_transpose2d_naive"):
+        sig(name, None, _f32p, _sz, _sz, _sz, _f32p, _sz, _sz, _sz, _sz, _f32p, _f32p)
+    for name in ("vko_bilinear_resize", "vko_bilinear_resize_naive",
+                 "vko_bilinear_resize_align_corners"):
+        sig(name, None, _f32p, _sz, _sz, _sz, _sz, _sz, _f32p)
     for name in ("vko_vit_block", "vko_vit_block_q8_0"):
         sig(name, None, _f32p, _sz, _sz, ctypes.POINTER(BlockWeights), _i64p,
             ctypes.c_float, ctypes.c_float, _f32p, _f32p, _f32p)
@@ -366,6 +373,82 @@ def hnd_to_token(hnd, tokens, heads, hd):
     x = f32(hnd)
     out = np.empty(tokens * heads * hd, np.float32)
     lib().vko_hnd_to_token(_f(x), tokens, heads, hd, _f(out))
+    return out
+
+
+# ---- DPT head ----------------------------------------------------------------
+def _opt(a):
+    return None if a is None else f32(a)
+
+
+def conv_out_hw(ih, iw, kh, kw, stride, pad):
+    return (ih + 2 * pad - kh) // stride + 1, (iw + 2 * pad - kw) // stride + 1
+
+
+def conv2d_naive(x, in_c, ih, iw, w, out_c, kh, kw, stride, pad, bias=None):
+    """conv::conv2d_naive (src/conv.rs:950-998), CHW, weight OIHW."""
+    oh, ow = conv_out_hw(ih, iw, kh, kw, stride, pad)
+    out = np.empty(out_c * oh * ow, np.float32)
+    b = _opt(bias)
+    lib().vko_conv2d_naive(_f(f32(x)), in_c, ih, iw, _f(f32(w)), out_c, kh, kw, stride, pad,
+                           _f(b) if b is not None else None, _f(out))
+    return out
+
+
+def _conv_t(fn, x, in_c, ih, iw, w, out_c, kh, kw, stride, bias):
+    oh, ow = (ih - 1) * stride + kh, (iw - 1) * stride + kw
+    out = np.empty(out_c * oh * ow, np.float32)
+    b = _opt(bias)
+    fn(_f(f32(x)), in_c, ih, iw, _f(f32(w)), out_c, kh, kw, stride,
+       _f(b) if b is not None else None, _f(out))
+    return out
+
+
+def conv_transpose2d(x, in_c, ih, iw, w, out_c, kh, kw, stride, bias=None):
+    """conv::conv_transpose2d (src/conv.rs:1009-1098), weight IOHW."""
+    return _conv_t(lib().vko_conv_transpose2d, x, in_c, ih, iw, w, out_c, kh, kw, stride, bias)
+
+
+def conv_transpose2d_naive(x, in_c, ih, iw, w, out_c, kh, kw, stride, bias=None):
+    """The crate's gather-form test oracle (src/conv.rs:1646-1704)."""
+    return _conv_t(lib().vko_conv_transpose2d_naive, x, in_c, ih, iw, w, out_c, kh, kw, stride,
+                   bias)
+
+
+def _resize(fn, x, c, ih, iw, oh, ow):
+    out = np.zeros(c * oh * ow, np.float32)
+    fn(_f(f32(x)), c, ih, iw, oh, ow, _f(out))
+    return out
+
+
+def bilinear_resize(x, c, ih, iw, oh, ow):
+    """resample::bilinear_resize (src/resample.rs:10-77), half-pixel centres."""
+    return _resize(lib().vko_bilinear_resize, x, c, ih, iw, oh, ow)
+
+
+def bilinear_resize_naive(x, c, ih, iw, oh, ow):
+    """resample::bilinear_resize_naive (src/resample.rs:101-149)."""
+    return _resize(lib().vko_bilinear_resize_naive, x, c, ih, iw, oh, ow)
+
+
+def bilinear_resize_align_corners(x, c, ih, iw, oh, ow):
+    """resample::bilinear_resize_align_corners (src/resample.rs:184-245)."""
+    return _resize(lib().vko_bilinear_resize_align_corners, x, c, ih, iw, oh, ow)
+
+
+def xorshift32_vec(seed, n):
+    """The reference tests' Xorshift32 data generator (src/conv.rs:1626-1640,
+    src/resample.rs:330-345): x ^= x<<13, x ^= x>>17, x ^= x<<5 (u32), then
+    (x as f32 / u32::MAX as f32) * 2 - 1, rounded as f32 at every step."""
+    x = seed & 0xFFFFFFFF
+    out = np.empty(n, np.float32)
+    umax = np.float32(4294967295.0)
+    for i in range(n):
+        x ^= (x << 13) & 0xFFFFFFFF
+        x ^= x >> 17
+        x ^= (x << 5) & 0xFFFFFFFF
+        v = np.float32(np.float32(x) / umax)
+        out[i] = np.float32(np.float32(v * np.float32(2.0)) - np.float32(1.0))
     return out
 
 

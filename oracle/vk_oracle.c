@@ -1274,3 +1274,248 @@ void vko_vit_block_q8_0(float *x_all, size_t images, size_t tokens, const vko_bl
     vit_block_impl(x_all, images, tokens, w, pos_yx, rope_freq, eps, tap_ln1, tap_attn, tap_gelu,
                    1);
 }
+
+/* ------------------------------------------------------------------------ */
+/* DPT head: convolution, transposed convolution, bilinear resize           */
+/* ------------------------------------------------------------------------ */
+
+/* conv::conv2d_naive (src/conv.rs:950-998): direct definition, taps outside
+ * the padded input skipped, acc += iv*wv unfused in (ic, ky, kx) order, then
+ * the bias.  Output channels run in parallel (each output keeps its order). */
+void vko_conv2d_naive(const float *input, size_t in_c, size_t ih, size_t iw, const float *weight,
+                      size_t out_c, size_t kh, size_t kw, size_t stride, size_t pad,
+                      const float *bias, float *out) {
+    const size_t oh = (ih + 2 * pad - kh) / stride + 1, ow = (iw + 2 * pad - kw) / stride + 1;
+#pragma omp parallel for OMP_THREADS schedule(static)
+    for (size_t oc = 0; oc < out_c; oc++)
+        for (size_t oy = 0; oy < oh; oy++)
+            for (size_t ox = 0; ox < ow; ox++) {
+                float acc = 0.0f;
+                for (size_t ic = 0; ic < in_c; ic++)
+                    for (size_t ky = 0; ky < kh; ky++) {
+                        const long iy = (long)(oy * stride + ky) - (long)pad;
+                        if (iy < 0 || iy >= (long)ih) continue;
+                        for (size_t kx = 0; kx < kw; kx++) {
+                            const long ix = (long)(ox * stride + kx) - (long)pad;
+                            if (ix < 0 || ix >= (long)iw) continue;
+                            const float iv = input[(ic * ih + (size_t)iy) * iw + (size_t)ix];
+                            const float wv = weight[((oc * in_c + ic) * kh + ky) * kw + kx];
+                            acc = acc + iv * wv;
+                        }
+                    }
+                if (bias) acc = acc + bias[oc];
+                out[(oc * oh + oy) * ow + ox] = acc;
+            }
+}
+
+/* conv::conv_transpose2d (src/conv.rs:1009-1098), its three routes:
+ *  - kernel == stride and in_c % 16 == 0 on an AVX-512 host: the prepacked
+ *    non-overlap kernel (src/specialized.rs:206-271): sixteen FMA lanes over
+ *    the input channels, lanes summed in order from -0.0, then + bias;
+ *  - kernel == stride otherwise: per output element the unfused sum over the
+ *    input channels, then + bias (src/conv.rs:1040-1070);
+ *  - otherwise the serial scatter from zero, skipping zero inputs, then
+ *    + bias (src/conv.rs:1072-1097). */
+void vko_conv_transpose2d(const float *input, size_t in_c, size_t ih, size_t iw,
+                          const float *weight, size_t out_c, size_t kh, size_t kw, size_t stride,
+                          const float *bias, float *out) {
+    const size_t oh = (ih - 1) * stride + kh, ow = (iw - 1) * stride + kw;
+    if (kh == stride && kw == stride && in_c % 16 == 0 && vko_has_avx512()) {
+#pragma omp parallel for OMP_THREADS schedule(static)
+        for (size_t oc = 0; oc < out_c; oc++) {
+            const float b = bias ? bias[oc] : 0.0f;
+            for (size_t iy = 0; iy < ih; iy++)
+                for (size_t ix = 0; ix < iw; ix++)
+                    for (size_t ky = 0; ky < kh; ky++)
+                        for (size_t kx = 0; kx < kw; kx++) {
+                            float lanes[16] = {0};
+                            for (size_t c0 = 0; c0 < in_c; c0 += 16)
+                                for (int l = 0; l < 16; l++) {
+                                    const size_t ic = c0 + (size_t)l;
+                                    lanes[l] = fmaf(input[(ic * ih + iy) * iw + ix],
+                                                    weight[((ic * out_c + oc) * kh + ky) * kw + kx],
+                                                    lanes[l]);
+                                }
+                            float sum = RUST_SUM_INIT;
+                            for (int l = 0; l < 16; l++) sum = sum + lanes[l];
+                            out[(oc * oh + iy * kh + ky) * ow + ix * kw + kx] = sum + b;
+                        }
+        }
+        return;
+    }
+    if (kh == stride && kw == stride) {
+#pragma omp parallel for OMP_THREADS schedule(static)
+        for (size_t oc = 0; oc < out_c; oc++) {
+            float *plane = out + oc * oh * ow;
+            for (size_t iy = 0; iy < ih; iy++)
+                for (size_t ix = 0; ix < iw; ix++)
+                    for (size_t ky = 0; ky < kh; ky++)
+                        for (size_t kx = 0; kx < kw; kx++) {
+                            float sum = 0.0f;
+                            for (size_t ic = 0; ic < in_c; ic++)
+                                sum = sum + input[(ic * ih + iy) * iw + ix] *
+                                                weight[((ic * out_c + oc) * kh + ky) * kw + kx];
+                            plane[(iy * stride + ky) * ow + ix * stride + kx] = sum;
+                        }
+            if (bias)
+                for (size_t i = 0; i < oh * ow; i++) plane[i] = plane[i] + bias[oc];
+        }
+        return;
+    }
+    memset(out, 0, out_c * oh * ow * sizeof(float));
+    for (size_t ic = 0; ic < in_c; ic++)
+        for (size_t iy = 0; iy < ih; iy++)
+            for (size_t ix = 0; ix < iw; ix++) {
+                const float iv = input[(ic * ih + iy) * iw + ix];
+                if (iv == 0.0f) continue;
+                for (size_t oc = 0; oc < out_c; oc++)
+                    for (size_t ky = 0; ky < kh; ky++)
+                        for (size_t kx = 0; kx < kw; kx++) {
+                            float *o = &out[(oc * oh + iy * stride + ky) * ow + ix * stride + kx];
+                            *o = *o + iv * weight[((ic * out_c + oc) * kh + ky) * kw + kx];
+                        }
+            }
+    if (bias)
+        for (size_t oc = 0; oc < out_c; oc++)
+            for (size_t i = 0; i < oh * ow; i++) out[oc * oh * ow + i] = out[oc * oh * ow + i] + bias[oc];
+}
+
+/* The crate's gather-form test oracle conv_transpose2d_naive
+ * (src/conv.rs:1646-1704): per output, (ic, ky, kx) ascending over the taps
+ * that land on it, unfused, then the bias. */
+void vko_conv_transpose2d_naive(const float *input, size_t in_c, size_t ih, size_t iw,
+                                const float *weight, size_t out_c, size_t kh, size_t kw,
+                                size_t stride, const float *bias, float *out) {
+    const size_t oh = (ih - 1) * stride + kh, ow = (iw - 1) * stride + kw;
+#pragma omp parallel for OMP_THREADS schedule(static)
+    for (size_t oc = 0; oc < out_c; oc++)
+        for (size_t oy = 0; oy < oh; oy++)
+            for (size_t ox = 0; ox < ow; ox++) {
+                float acc = 0.0f;
+                for (size_t ic = 0; ic < in_c; ic++)
+                    for (size_t ky = 0; ky < kh; ky++) {
+                        if (oy < ky || (oy - ky) % stride) continue;
+                        const size_t iy = (oy - ky) / stride;
+                        if (iy >= ih) continue;
+                        for (size_t kx = 0; kx < kw; kx++) {
+                            if (ox < kx || (ox - kx) % stride) continue;
+                            const size_t ix = (ox - kx) / stride;
+                            if (ix >= iw) continue;
+                            acc = acc + input[(ic * ih + iy) * iw + ix] *
+                                            weight[((ic * out_c + oc) * kh + ky) * kw + kx];
+                        }
+                    }
+                if (bias) acc = acc + bias[oc];
+                out[(oc * oh + oy) * ow + ox] = acc;
+            }
+}
+
+typedef struct {
+    size_t i0, i1;
+    float frac;
+} vko_tap;
+
+/* Rust `f as usize` saturates: negative and NaN go to 0. */
+static inline size_t sat_usize(float f) { return f > 0.0f ? (size_t)f : 0; }
+
+/* resample::src_coord (src/resample.rs:82-95): half-pixel centres. */
+static vko_tap src_coord(size_t dst, float scale, size_t len_in) {
+    const float src = ((float)dst + 0.5f) * scale - 0.5f;
+    const float sc = rmax(src, 0.0f);
+    size_t i0 = sat_usize(floorf(sc));
+    const size_t last = len_in ? len_in - 1 : 0;
+    if (i0 > last) i0 = last;
+    const size_t i1 = i0 + 1 < last ? i0 + 1 : last;
+    float frac = i1 == i0 ? 0.0f : sc - (float)i0;
+    frac = fminf(fmaxf(frac, 0.0f), 1.0f);
+    vko_tap t = {i0, i1, frac};
+    return t;
+}
+
+/* resample::src_coord_align_corners (src/resample.rs:151-166). */
+static vko_tap src_coord_align_corners(size_t dst, size_t len_in, size_t len_out) {
+    vko_tap t = {0, 0, 0.0f};
+    if (len_in <= 1) return t;
+    float src = len_out <= 1 ? 0.0f : (float)dst * (float)(len_in - 1) / (float)(len_out - 1);
+    src = fminf(fmaxf(src, 0.0f), (float)(len_in - 1));
+    size_t i0 = sat_usize(floorf(src));
+    if (i0 > len_in - 1) i0 = len_in - 1;
+    const size_t i1 = i0 + 1 < len_in - 1 ? i0 + 1 : len_in - 1;
+    float frac = i1 == i0 ? 0.0f : src - (float)i0;
+    t.i0 = i0;
+    t.i1 = i1;
+    t.frac = fminf(fmaxf(frac, 0.0f), 1.0f);
+    return t;
+}
+
+static void bilinear_tables(const float *input, size_t c, size_t ih, size_t iw, size_t oh,
+                            size_t ow, const vko_tap *ty, const vko_tap *tx, float *out) {
+#pragma omp parallel for OMP_THREADS schedule(static)
+    for (size_t ch = 0; ch < c; ch++) {
+        const float *plane = input + ch * ih * iw;
+        for (size_t oy = 0; oy < oh; oy++) {
+            const float *row0 = plane + ty[oy].i0 * iw, *row1 = plane + ty[oy].i1 * iw;
+            const float fy = ty[oy].frac;
+            for (size_t ox = 0; ox < ow; ox++) {
+                const size_t x0 = tx[ox].i0, x1 = tx[ox].i1;
+                const float fx = tx[ox].frac;
+                const float top = row0[x0] * (1.0f - fx) + row0[x1] * fx;
+                const float bot = row1[x0] * (1.0f - fx) + row1[x1] * fx;
+                out[(ch * oh + oy) * ow + ox] = top * (1.0f - fy) + bot * fy;
+            }
+        }
+    }
+}
+
+/* resample::bilinear_resize (src/resample.rs:10-77): per-axis tables, then
+ * the two-row blend.  Empty input or output: out is left untouched. */
+void vko_bilinear_resize(const float *input, size_t c, size_t ih, size_t iw, size_t oh, size_t ow,
+                         float *out) {
+    if (!ih || !iw || !oh || !ow) return;
+    const float sy = (float)ih / (float)oh, sx = (float)iw / (float)ow;
+    vko_tap *ty = (vko_tap *)malloc(oh * sizeof(vko_tap)), *tx = (vko_tap *)malloc(ow * sizeof(vko_tap));
+    for (size_t y = 0; y < oh; y++) ty[y] = src_coord(y, sy, ih);
+    for (size_t x = 0; x < ow; x++) tx[x] = src_coord(x, sx, iw);
+    bilinear_tables(input, c, ih, iw, oh, ow, ty, tx, out);
+    free(ty);
+    free(tx);
+}
+
+/* resample::bilinear_resize_naive (src/resample.rs:101-149): coordinates
+ * recomputed for every output element. */
+void vko_bilinear_resize_naive(const float *input, size_t c, size_t ih, size_t iw, size_t oh,
+                               size_t ow, float *out) {
+    if (!ih || !iw || !oh || !ow) return;
+    const float scale_y = (float)ih / (float)oh, scale_x = (float)iw / (float)ow;
+    for (size_t ch = 0; ch < c; ch++)
+        for (size_t oy = 0; oy < oh; oy++) {
+            const float sy = rmax(((float)oy + 0.5f) * scale_y - 0.5f, 0.0f);
+            size_t y0 = sat_usize(floorf(sy));
+            if (y0 > ih - 1) y0 = ih - 1;
+            const size_t y1 = y0 + 1 < ih - 1 ? y0 + 1 : ih - 1;
+            const float fy = y1 == y0 ? 0.0f : fminf(fmaxf(sy - (float)y0, 0.0f), 1.0f);
+            for (size_t ox = 0; ox < ow; ox++) {
+                const float sx = rmax(((float)ox + 0.5f) * scale_x - 0.5f, 0.0f);
+                size_t x0 = sat_usize(floorf(sx));
+                if (x0 > iw - 1) x0 = iw - 1;
+                const size_t x1 = x0 + 1 < iw - 1 ? x0 + 1 : iw - 1;
+                const float fx = x1 == x0 ? 0.0f : fminf(fmaxf(sx - (float)x0, 0.0f), 1.0f);
+                const float *p = input + ch * ih * iw;
+                const float top = p[y0 * iw + x0] * (1.0f - fx) + p[y0 * iw + x1] * fx;
+                const float bot = p[y1 * iw + x0] * (1.0f - fx) + p[y1 * iw + x1] * fx;
+                out[(ch * oh + oy) * ow + ox] = top * (1.0f - fy) + bot * fy;
+            }
+        }
+}
+
+/* resample::bilinear_resize_align_corners (src/resample.rs:184-245). */
+void vko_bilinear_resize_align_corners(const float *input, size_t c, size_t ih, size_t iw,
+                                       size_t oh, size_t ow, float *out) {
+    if (!ih || !iw || !oh || !ow) return;
+    vko_tap *ty = (vko_tap *)malloc(oh * sizeof(vko_tap)), *tx = (vko_tap *)malloc(ow * sizeof(vko_tap));
+    for (size_t y = 0; y < oh; y++) ty[y] = src_coord_align_corners(y, ih, oh);
+    for (size_t x = 0; x < ow; x++) tx[x] = src_coord_align_corners(x, iw, ow);
+    bilinear_tables(input, c, ih, iw, oh, ow, ty, tx, out);
+    free(ty);
+    free(tx);
+}

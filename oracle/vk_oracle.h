@@ -152,6 +152,29 @@ void vko_vit_block_q8_0(float *x, size_t images, size_t tokens, const vko_block_
                         const int64_t *pos_yx, float rope_freq, float eps, float *tap_ln1,
                         float *tap_attn, float *tap_gelu);
 
+/* ---- DPT head (src/conv.rs, src/resample.rs); batch-1 CHW ------------- */
+/* conv2d_naive (src/conv.rs:950-998): weight OIHW, bias [out_c] or NULL,
+ * oh = (ih + 2*pad - kh)/stride + 1. */
+void vko_conv2d_naive(const float *input, size_t in_c, size_t ih, size_t iw, const float *weight,
+                      size_t out_c, size_t kh, size_t kw, size_t stride, size_t pad,
+                      const float *bias, float *out);
+/* conv_transpose2d (src/conv.rs:1009-1098) with its three routes; weight
+ * IOHW, oh = (ih-1)*stride + kh. */
+void vko_conv_transpose2d(const float *input, size_t in_c, size_t ih, size_t iw,
+                          const float *weight, size_t out_c, size_t kh, size_t kw, size_t stride,
+                          const float *bias, float *out);
+/* The gather-form test oracle of src/conv.rs:1646-1704. */
+void vko_conv_transpose2d_naive(const float *input, size_t in_c, size_t ih, size_t iw,
+                                const float *weight, size_t out_c, size_t kh, size_t kw,
+                                size_t stride, const float *bias, float *out);
+/* src/resample.rs: half-pixel (table and per-element forms) and align-corners. */
+void vko_bilinear_resize(const float *input, size_t c, size_t ih, size_t iw, size_t oh, size_t ow,
+                         float *out);
+void vko_bilinear_resize_naive(const float *input, size_t c, size_t ih, size_t iw, size_t oh,
+                               size_t ow, float *out);
+void vko_bilinear_resize_align_corners(const float *input, size_t c, size_t ih, size_t iw,
+                                       size_t oh, size_t ow, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -59,6 +59,29 @@ hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k,
                                   float *out, size_t bh, size_t tokens, size_t heads,
                                   bool token_major, float *ws, size_t ws_floats);
 
+// ---- DPT head (k_dpt.hip) ------------------------------------------------
+// colT [oh*ow][in_c*kh*kw] of a CHW input (zero padding; ReLU on the input
+// values when relu).
+hipError_t launch_im2col_t(hipStream_t s, const float *in, float *col, size_t in_c, size_t ih,
+                           size_t iw, size_t kh, size_t kw, size_t stride, size_t pad, size_t oh,
+                           size_t ow, bool relu);
+// c [ih*iw][out_c*kh*kw] -> out [out_c][ih*kh][iw*kw] (kernel == stride).
+hipError_t launch_patch_scatter(hipStream_t s, const float *c, float *out, size_t out_c,
+                                size_t ih, size_t iw, size_t kh, size_t kw);
+// Transposed convolution of any kernel and stride (IOHW weight), gathered
+// per output element; bias may be null.
+hipError_t launch_conv_transpose_gather(hipStream_t s, const float *in, const float *w,
+                                        const float *bias, float *out, size_t in_c, size_t ih,
+                                        size_t iw, size_t out_c, size_t kh, size_t kw,
+                                        size_t stride);
+// Bilinear resize of c CHW planes (half-pixel centres or align-corners), then
+// + add (same shape as out) when add is non-null.
+hipError_t launch_bilinear(hipStream_t s, const float *in, const float *add, float *out,
+                           size_t c, size_t ih, size_t iw, size_t oh, size_t ow,
+                           bool align_corners);
+// p[0..n) = v (a kernel, so that it may sit in a captured graph).
+hipError_t launch_fill(hipStream_t s, float *p, size_t n, float v);
+
 // ---- GEMM (k_gemm.hip) ----------------------------------------------------
 enum class Epi : int { Store = 0, Gelu = 1, Residual = 2, Qkv = 3 };
 

@@ -1844,6 +1844,415 @@ extern "C" vh_status vh_encoder_run(const vh_runtime *rt, const vh_block *const 
 }
 
 // =============================================================================
+// DPT head: convolution, transposed convolution, bilinear resize
+// =============================================================================
+
+struct vh_conv2d {
+    Rt rt;
+    size_t in_c = 0, out_c = 0, kh = 0, kw = 0, stride = 0, pad = 0;
+    float *w = nullptr;     // OIHW = [out_c][in_c*kh*kw], the GEMM's Bt operand
+    float *bias = nullptr;  // [out_c] or null
+    ~vh_conv2d() {
+        if (!rt) return;
+        hipSetDevice(rt->device);
+        for (float *p : {w, bias})
+            if (p) hipFreeAsync(p, rt->stream);
+    }
+};
+
+struct vh_conv_transpose2d {
+    Rt rt;
+    size_t in_c = 0, out_c = 0, kh = 0, kw = 0, stride = 0;
+    bool nonoverlap = false;  // kernel == stride: one GEMM plus a patch scatter
+    float *w = nullptr;       // nonoverlap: [out_c*kh*kw][in_c]; else IOHW as given
+    float *bias = nullptr;    // [out_c] or null
+    float *bias_x = nullptr;  // nonoverlap: bias repeated per (ky, kx), [out_c*kh*kw]
+    ~vh_conv_transpose2d() {
+        if (!rt) return;
+        hipSetDevice(rt->device);
+        for (float *p : {w, bias, bias_x})
+            if (p) hipFreeAsync(p, rt->stream);
+    }
+};
+
+namespace {
+
+vh_status check_tensor_len(const vh_tensor *t, size_t expected, const char *what) {
+    if (t->len != expected) return mismatch(t->len, expected, what);
+    return VH_OK;
+}
+
+// c [rows][cols] = a [rows][k] . bt [cols][k]^T (+ bias[col]), the fp32-MFMA GEMM.
+vh_status gemm_nt(RtState &s, const float *a, const float *bt, const float *bias, float *c,
+                  size_t rows, size_t cols, size_t k, const char *name) {
+    vh::GemmArgs g{};
+    g.a = a;
+    g.bt = bt;
+    g.m = rows;
+    g.n = cols;
+    g.k = k;
+    g.epi = vh::Epi::Store;
+    g.c = c;
+    g.bias = bias;
+    TRY(splitk_workspace(s, rows, cols, &g.ws, &g.ws_floats));
+    return launch(s, name, [&] { return vh::launch_gemm(s.stream, g); });
+}
+
+// Convolution of a CHW input in place of conv2d (src/conv.rs:877-945): the
+// patches as colT [pixels][K], one GEMM against the OIHW weight with the
+// bias in its epilogue, then [pixels][out_c] -> CHW.
+vh_status conv_run(RtState &s, const vh_conv2d &c, const float *in, size_t ih, size_t iw,
+                   bool relu, float *out) {
+    const size_t oh = (ih + 2 * c.pad - c.kh) / c.stride + 1;
+    const size_t ow = (iw + 2 * c.pad - c.kw) / c.stride + 1;
+    const size_t npix = oh * ow, K = c.in_c * c.kh * c.kw;
+    float *col = nullptr, *tmp = nullptr;
+    vh_status st = dalloc(s, npix * K, &col, "convolution patch allocation");
+    if (!st) st = dalloc(s, npix * c.out_c, &tmp, "convolution output allocation");
+    if (!st) {
+        const bool plain = c.kh == 1 && c.kw == 1 && c.stride == 1 && c.pad == 0 && !relu;
+        st = launch(s, plain ? "transpose" : "im2col", [&] {
+            return plain ? vh::launch_transpose(s.stream, in, col, c.in_c, npix)
+                         : vh::launch_im2col_t(s.stream, in, col, c.in_c, ih, iw, c.kh, c.kw,
+                                               c.stride, c.pad, oh, ow, relu);
+        });
+    }
+    if (!st) st = gemm_nt(s, col, c.w, c.bias, tmp, npix, c.out_c, K, "conv_gemm");
+    if (!st)
+        st = launch(s, "transpose", [&] {
+            return vh::launch_transpose(s.stream, tmp, out, npix, c.out_c);
+        });
+    if (col) hipFreeAsync(col, s.stream);
+    if (tmp) hipFreeAsync(tmp, s.stream);
+    return st;
+}
+
+vh_status conv_geometry(const vh_conv2d *c, const vh_tensor *input, size_t ih, size_t iw,
+                        size_t *oh, size_t *ow) {
+    size_t plane = 0, len = 0;
+    if (mul_overflows(ih, iw, &plane) || mul_overflows(plane, c->in_c, &len))
+        return fail(VH_ERR_KERNEL, "conv2d: input size overflows");
+    TRY(check_tensor_len(input, len, "conv2d input"));
+    if (ih + 2 * c->pad < c->kh || iw + 2 * c->pad < c->kw)
+        return fail(VH_ERR_KERNEL, "conv2d: kernel larger than the padded input");
+    *oh = (ih + 2 * c->pad - c->kh) / c->stride + 1;
+    *ow = (iw + 2 * c->pad - c->kw) / c->stride + 1;
+    size_t npix = *oh * *ow, cells = 0, outs = 0;
+    if (mul_overflows(npix, c->in_c * c->kh * c->kw, &cells) || cells > (size_t)INT32_MAX ||
+        mul_overflows(npix, c->out_c, &outs) || outs > (size_t)INT32_MAX ||
+        npix > (size_t)INT32_MAX / 2 || ih > INT32_MAX / 2 || iw > INT32_MAX / 2 ||
+        (npix + 31) / 32 > 65535)
+        return fail(VH_ERR_KERNEL, "conv2d: shape exceeds the supported size");
+    return VH_OK;
+}
+
+vh_status prepare_conv(const vh_runtime *rt, size_t in_c, size_t out_c, size_t kh, size_t kw,
+                       size_t stride, size_t pad, const float *weight, const float *bias,
+                       vh_conv2d **out) {
+    NEED(rt, "vh_prepare_conv2d_f32");
+    NEED(out, "vh_prepare_conv2d_f32");
+    if (!in_c || !out_c || !kh || !kw || !stride)
+        return fail(VH_ERR_KERNEL, "conv2d: channels, kernel and stride must be non-zero");
+    size_t n = 0;
+    if (mul_overflows(out_c, in_c * kh * kw, &n) || in_c > INT32_MAX / (kh * kw) ||
+        out_c > INT32_MAX)
+        return fail(VH_ERR_KERNEL, "conv2d: weight size overflows");
+    NEED(weight, "vh_prepare_conv2d_f32 weight");
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_conv2d *c = new vh_conv2d;
+    c->rt = rt->s;
+    c->in_c = in_c;
+    c->out_c = out_c;
+    c->kh = kh;
+    c->kw = kw;
+    c->stride = stride;
+    c->pad = pad;
+    vh_status st = upload_array(s, weight, n, &c->w, "conv2d weight upload");
+    if (!st && bias) st = upload_array(s, bias, out_c, &c->bias, "conv2d bias upload");
+    if (st) {
+        delete c;
+        return st;
+    }
+    *out = c;
+    return VH_OK;
+}
+
+vh_status conv_new(const vh_conv2d *conv, const vh_tensor *input, size_t ih, size_t iw,
+                   bool relu, vh_tensor **out, const char *name) {
+    NEED(conv, name);
+    NEED(input, name);
+    NEED(out, name);
+    size_t oh = 0, ow = 0;
+    TRY(conv_geometry(conv, input, ih, iw, &oh, &ow));
+    RtState &s = *conv->rt;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(conv->rt, conv->out_c * oh * ow, &t, "conv2d output allocation"));
+    vh_status st = conv_run(s, *conv, input->ptr, ih, iw, relu, t->ptr);
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+}
+
+vh_status prepare_conv_t(const vh_runtime *rt, size_t in_c, size_t out_c, size_t kh, size_t kw,
+                         size_t stride, const float *weight, const float *bias,
+                         vh_conv_transpose2d **out) {
+    NEED(rt, "vh_prepare_conv_transpose2d_f32");
+    NEED(out, "vh_prepare_conv_transpose2d_f32");
+    if (!in_c || !out_c || !kh || !kw || !stride)
+        return fail(VH_ERR_KERNEL, "conv_transpose2d: channels, kernel and stride must be non-zero");
+    size_t n = 0;
+    if (mul_overflows(in_c, out_c * kh * kw, &n) || out_c * kh * kw > INT32_MAX ||
+        in_c > INT32_MAX)
+        return fail(VH_ERR_KERNEL, "conv_transpose2d: weight size overflows");
+    NEED(weight, "vh_prepare_conv_transpose2d_f32 weight");
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_conv_transpose2d *c = new vh_conv_transpose2d;
+    c->rt = rt->s;
+    c->in_c = in_c;
+    c->out_c = out_c;
+    c->kh = kh;
+    c->kw = kw;
+    c->stride = stride;
+    c->nonoverlap = kh == stride && kw == stride;
+    vh_status st = VH_OK;
+    if (c->nonoverlap) {
+        // prepare_nonoverlap_transpose_f32 (src/specialized.rs:148-174): IOHW
+        // -> [out_c][kh][kw][in_c], the GEMM's Bt operand.
+        std::vector<float> packed(n);
+        const size_t taps = kh * kw;
+        for (size_t o = 0; o < out_c; o++)
+            for (size_t t = 0; t < taps; t++)
+                for (size_t i = 0; i < in_c; i++)
+                    packed[(o * taps + t) * in_c + i] = weight[(i * out_c + o) * taps + t];
+        st = upload_array(s, packed.data(), n, &c->w, "conv_transpose2d weight upload");
+        if (!st && bias) {
+            std::vector<float> bx(out_c * taps);
+            for (size_t o = 0; o < out_c; o++)
+                for (size_t t = 0; t < taps; t++) bx[o * taps + t] = bias[o];
+            st = upload_array(s, bx.data(), bx.size(), &c->bias_x, "conv_transpose2d bias upload");
+        }
+    } else {
+        st = upload_array(s, weight, n, &c->w, "conv_transpose2d weight upload");
+        if (!st && bias) st = upload_array(s, bias, out_c, &c->bias, "conv_transpose2d bias upload");
+    }
+    if (st) {
+        delete c;
+        return st;
+    }
+    *out = c;
+    return VH_OK;
+}
+
+vh_status conv_t_new(const vh_conv_transpose2d *c, const vh_tensor *input, size_t ih, size_t iw,
+                     vh_tensor **out) {
+    NEED(c, "vh_conv_transpose2d_run");
+    NEED(input, "vh_conv_transpose2d_run");
+    NEED(out, "vh_conv_transpose2d_run");
+    size_t plane = 0, len = 0;
+    if (mul_overflows(ih, iw, &plane) || mul_overflows(plane, c->in_c, &len))
+        return fail(VH_ERR_KERNEL, "conv_transpose2d: input size overflows");
+    TRY(check_tensor_len(input, len, "conv_transpose2d input"));
+    if (ih == 0 || iw == 0)
+        return fail(VH_ERR_KERNEL, "conv_transpose2d: empty input (the output size needs ih, iw >= 1)");
+    const size_t oh = (ih - 1) * c->stride + c->kh, ow = (iw - 1) * c->stride + c->kw;
+    size_t olen = 0;
+    if (mul_overflows(oh, ow, &olen) || mul_overflows(olen, c->out_c, &olen) ||
+        olen > (size_t)INT32_MAX * 4 || oh > INT32_MAX / 2 || ow > INT32_MAX / 2 ||
+        (plane + 31) / 32 > 65535)
+        return fail(VH_ERR_KERNEL, "conv_transpose2d: shape exceeds the supported size");
+    GUARD_BEGIN
+    RtState &s = *c->rt;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(c->rt, olen, &t, "conv_transpose2d output allocation"));
+    vh_status st = VH_OK;
+    if (c->nonoverlap) {
+        const size_t cols = c->out_c * c->kh * c->kw;
+        float *xt = nullptr, *tmp = nullptr;
+        st = dalloc(s, plane * c->in_c, &xt, "conv_transpose2d staging allocation");
+        if (!st) st = dalloc(s, plane * cols, &tmp, "conv_transpose2d staging allocation");
+        if (!st)
+            st = launch(s, "transpose", [&] {
+                return vh::launch_transpose(s.stream, input->ptr, xt, c->in_c, plane);
+            });
+        if (!st) st = gemm_nt(s, xt, c->w, c->bias_x, tmp, plane, cols, c->in_c, "conv_transpose_gemm");
+        if (!st)
+            st = launch(s, "patch_scatter", [&] {
+                return vh::launch_patch_scatter(s.stream, tmp, t->ptr, c->out_c, ih, iw, c->kh, c->kw);
+            });
+        if (xt) hipFreeAsync(xt, s.stream);
+        if (tmp) hipFreeAsync(tmp, s.stream);
+    } else {
+        st = launch(s, "conv_transpose_gather", [&] {
+            return vh::launch_conv_transpose_gather(s.stream, input->ptr, c->w, c->bias, t->ptr,
+                                                    c->in_c, ih, iw, c->out_c, c->kh, c->kw,
+                                                    c->stride);
+        });
+    }
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+vh_status resize_new(const vh_runtime *rt, const vh_tensor *input, size_t c, size_t ih,
+                     size_t iw, size_t oh, size_t ow, const vh_tensor *add, bool align,
+                     vh_tensor **out, const char *name) {
+    NEED(rt, name);
+    NEED(input, name);
+    NEED(out, name);
+    size_t ilen = 0, olen = 0;
+    if (mul_overflows(c, ih, &ilen) || mul_overflows(ilen, iw, &ilen) ||
+        mul_overflows(c, oh, &olen) || mul_overflows(olen, ow, &olen))
+        return fail(VH_ERR_KERNEL, std::string(name) + ": size overflows");
+    TRY(check_tensor_len(input, ilen, name));
+    if (add) TRY(check_tensor_len(add, olen, name));
+    if (c > INT32_MAX || ih > INT32_MAX || iw > INT32_MAX || oh > INT32_MAX || ow > INT32_MAX)
+        return fail(VH_ERR_KERNEL, std::string(name) + ": dimension exceeds 2^31-1");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    vh_tensor *t = nullptr;
+    TRY(new_tensor(rt->s, olen, &t, "resize output allocation"));
+    // src/resample.rs returns without writing for an empty input or output.
+    vh_status st = VH_OK;
+    if (olen && ilen) {
+        st = launch(s, align ? "bilinear_align_corners" : "bilinear", [&] {
+            return vh::launch_bilinear(s.stream, input->ptr, add ? add->ptr : nullptr, t->ptr, c,
+                                       ih, iw, oh, ow, align);
+        });
+    } else if (olen) {
+        st = launch(s, "fill", [&] { return vh::launch_fill(s.stream, t->ptr, olen, 0.0f); });
+    }
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+}  // namespace
+
+extern "C" vh_status vh_prepare_conv2d_f32(const vh_runtime *rt, size_t in_c, size_t out_c,
+                                           size_t kh, size_t kw, size_t stride, size_t pad,
+                                           const float *weight, const float *bias,
+                                           vh_conv2d **out) {
+    GUARD_BEGIN
+    return prepare_conv(rt, in_c, out_c, kh, kw, stride, pad, weight, bias, out);
+    GUARD_END
+}
+
+extern "C" void vh_conv2d_free(vh_conv2d *conv) { delete conv; }
+
+extern "C" vh_status vh_conv2d_run(const vh_conv2d *conv, const vh_tensor *input, size_t ih,
+                                   size_t iw, vh_tensor **out) {
+    GUARD_BEGIN
+    return conv_new(conv, input, ih, iw, false, out, "vh_conv2d_run");
+    GUARD_END
+}
+
+extern "C" vh_status vh_conv2d_run_relu_input(const vh_conv2d *conv, const vh_tensor *input,
+                                              size_t ih, size_t iw, vh_tensor **out) {
+    GUARD_BEGIN
+    return conv_new(conv, input, ih, iw, true, out, "vh_conv2d_run_relu_input");
+    GUARD_END
+}
+
+extern "C" vh_status vh_conv2d_run_resize_align_corners(const vh_conv2d *conv,
+                                                        const vh_tensor *input, size_t ih,
+                                                        size_t iw, size_t oh, size_t ow,
+                                                        const vh_tensor *add, vh_tensor **out) {
+    NEED(conv, "vh_conv2d_run_resize_align_corners");
+    GUARD_BEGIN
+    vh_runtime rt{conv->rt};
+    vh_tensor *resized = nullptr;
+    TRY(resize_new(&rt, input, conv->in_c, ih, iw, oh, ow, add, true, &resized,
+                   "vh_conv2d_run_resize_align_corners"));
+    vh_status st = conv_new(conv, resized, oh, ow, false, out, "vh_conv2d_run_resize_align_corners");
+    delete resized;
+    return st;
+    GUARD_END
+}
+
+extern "C" vh_status vh_conv2d_f32(const vh_runtime *rt, const vh_tensor *input, size_t in_c,
+                                   size_t ih, size_t iw, const float *weight, size_t out_c,
+                                   size_t kh, size_t kw, size_t stride, size_t pad,
+                                   const float *bias, vh_tensor **out) {
+    GUARD_BEGIN
+    vh_conv2d *c = nullptr;
+    TRY(prepare_conv(rt, in_c, out_c, kh, kw, stride, pad, weight, bias, &c));
+    vh_status st = conv_new(c, input, ih, iw, false, out, "vh_conv2d_f32");
+    delete c;
+    return st;
+    GUARD_END
+}
+
+extern "C" size_t vh_conv2d_output_height(const vh_conv2d *c, size_t ih) {
+    return c && ih + 2 * c->pad >= c->kh ? (ih + 2 * c->pad - c->kh) / c->stride + 1 : 0;
+}
+extern "C" size_t vh_conv2d_output_width(const vh_conv2d *c, size_t iw) {
+    return c && iw + 2 * c->pad >= c->kw ? (iw + 2 * c->pad - c->kw) / c->stride + 1 : 0;
+}
+
+extern "C" vh_status vh_prepare_conv_transpose2d_f32(const vh_runtime *rt, size_t in_c,
+                                                     size_t out_c, size_t kh, size_t kw,
+                                                     size_t stride, const float *weight,
+                                                     const float *bias,
+                                                     vh_conv_transpose2d **out) {
+    GUARD_BEGIN
+    return prepare_conv_t(rt, in_c, out_c, kh, kw, stride, weight, bias, out);
+    GUARD_END
+}
+
+extern "C" void vh_conv_transpose2d_free(vh_conv_transpose2d *conv) { delete conv; }
+
+extern "C" vh_status vh_conv_transpose2d_run(const vh_conv_transpose2d *conv,
+                                             const vh_tensor *input, size_t ih, size_t iw,
+                                             vh_tensor **out) {
+    return conv_t_new(conv, input, ih, iw, out);
+}
+
+extern "C" vh_status vh_conv_transpose2d_f32(const vh_runtime *rt, const vh_tensor *input,
+                                             size_t in_c, size_t ih, size_t iw,
+                                             const float *weight, size_t out_c, size_t kh,
+                                             size_t kw, size_t stride, const float *bias,
+                                             vh_tensor **out) {
+    GUARD_BEGIN
+    vh_conv_transpose2d *c = nullptr;
+    TRY(prepare_conv_t(rt, in_c, out_c, kh, kw, stride, weight, bias, &c));
+    vh_status st = conv_t_new(c, input, ih, iw, out);
+    delete c;
+    return st;
+    GUARD_END
+}
+
+extern "C" vh_status vh_bilinear_resize_f32(const vh_runtime *rt, const vh_tensor *input,
+                                            size_t c, size_t ih, size_t iw, size_t oh, size_t ow,
+                                            vh_tensor **out) {
+    return resize_new(rt, input, c, ih, iw, oh, ow, nullptr, false, out, "vh_bilinear_resize_f32");
+}
+
+extern "C" vh_status vh_bilinear_resize_align_corners_f32(const vh_runtime *rt,
+                                                          const vh_tensor *input, size_t c,
+                                                          size_t ih, size_t iw, size_t oh,
+                                                          size_t ow, const vh_tensor *add,
+                                                          vh_tensor **out) {
+    return resize_new(rt, input, c, ih, iw, oh, ow, add, true, out,
+                      "vh_bilinear_resize_align_corners_f32");
+}
+
+// =============================================================================
 // profiling
 // =============================================================================
 

@@ -136,6 +136,21 @@ SIGNATURES = [
     ("vh_linear_q8_0_run", _S, [_p, _p, _sz, _pp]),
     ("vh_linear_q8_0_run_gelu", _S, [_p, _p, _sz, _pp]),
     ("vh_linear_q8_0_run_residual", _S, [_p, _p, _sz, _p]),
+    ("vh_prepare_conv2d_f32", _S, [_p, _sz, _sz, _sz, _sz, _sz, _sz, _f32p, _f32p, _pp]),
+    ("vh_conv2d_free", None, [_p]),
+    ("vh_conv2d_output_height", _sz, [_p, _sz]),
+    ("vh_conv2d_output_width", _sz, [_p, _sz]),
+    ("vh_conv2d_run", _S, [_p, _p, _sz, _sz, _pp]),
+    ("vh_conv2d_run_relu_input", _S, [_p, _p, _sz, _sz, _pp]),
+    ("vh_conv2d_run_resize_align_corners", _S, [_p, _p, _sz, _sz, _sz, _sz, _p, _pp]),
+    ("vh_conv2d_f32", _S, [_p, _p, _sz, _sz, _sz, _f32p, _sz, _sz, _sz, _sz, _sz, _f32p, _pp]),
+    ("vh_prepare_conv_transpose2d_f32", _S, [_p, _sz, _sz, _sz, _sz, _sz, _f32p, _f32p, _pp]),
+    ("vh_conv_transpose2d_free", None, [_p]),
+    ("vh_conv_transpose2d_run", _S, [_p, _p, _sz, _sz, _pp]),
+    ("vh_conv_transpose2d_f32", _S, [_p, _p, _sz, _sz, _sz, _f32p, _sz, _sz, _sz, _sz, _f32p,
+                                     _pp]),
+    ("vh_bilinear_resize_f32", _S, [_p, _p, _sz, _sz, _sz, _sz, _sz, _pp]),
+    ("vh_bilinear_resize_align_corners_f32", _S, [_p, _p, _sz, _sz, _sz, _sz, _sz, _p, _pp]),
     ("vh_block_prepare", _S, [_p, _p, _pp]),
     ("vh_block_prepare_q8_0", _S, [_p, _p, _pp]),
     ("vh_block_is_q8_0", ctypes.c_int, [_p]),
@@ -343,6 +358,63 @@ class LinearQ8:
             pass
 
 
+class Conv2d:
+    """A prepared 2-D convolution (conv2d with a model-owned weight)."""
+
+    def __init__(self, runtime: "Runtime", handle: int):
+        self._rt = runtime
+        self._h = ctypes.c_void_p(handle)
+
+    def output_hw(self, ih: int, iw: int):
+        return (int(lib().vh_conv2d_output_height(self._h, ih)),
+                int(lib().vh_conv2d_output_width(self._h, iw)))
+
+    def _new(self, fn, *args) -> Tensor:
+        out = ctypes.c_void_p()
+        _check(fn(self._h, *args, ctypes.byref(out)))
+        return Tensor(self._rt, out.value)
+
+    def run(self, x: Tensor, ih: int, iw: int) -> Tensor:
+        return self._new(lib().vh_conv2d_run, x.handle, ih, iw)
+
+    def run_relu_input(self, x: Tensor, ih: int, iw: int) -> Tensor:
+        return self._new(lib().vh_conv2d_run_relu_input, x.handle, ih, iw)
+
+    def run_resize_align_corners(self, x: Tensor, ih: int, iw: int, oh: int, ow: int,
+                                 add: Tensor | None = None) -> Tensor:
+        return self._new(lib().vh_conv2d_run_resize_align_corners, x.handle, ih, iw, oh, ow,
+                         add.handle if add is not None else None)
+
+    def __del__(self):
+        try:
+            if self._h and self._h.value:
+                lib().vh_conv2d_free(self._h)
+                self._h = ctypes.c_void_p(None)
+        except Exception:
+            pass
+
+
+class ConvTranspose2d:
+    """A prepared transposed convolution (IOHW weight)."""
+
+    def __init__(self, runtime: "Runtime", handle: int):
+        self._rt = runtime
+        self._h = ctypes.c_void_p(handle)
+
+    def run(self, x: Tensor, ih: int, iw: int) -> Tensor:
+        out = ctypes.c_void_p()
+        _check(lib().vh_conv_transpose2d_run(self._h, x.handle, ih, iw, ctypes.byref(out)))
+        return Tensor(self._rt, out.value)
+
+    def __del__(self):
+        try:
+            if self._h and self._h.value:
+                lib().vh_conv_transpose2d_free(self._h)
+                self._h = ctypes.c_void_p(None)
+        except Exception:
+            pass
+
+
 class BlockParams(ctypes.Structure):
     _fields_ = [(n, _f32p) for n in da3.BLOCK_FIELDS + da3.QK_NORM_FIELDS]
 
@@ -542,6 +614,47 @@ class Runtime:
                                             _fp(g) if g is not None else None,
                                             ctypes.byref(out)))
         return LinearQ8(self, out.value)
+
+    # -- DPT head
+    def prepare_conv2d_f32(self, in_c, out_c, kh, kw, stride, pad, weight, bias=None) -> Conv2d:
+        w = _f32(weight).reshape(-1)
+        b = None if bias is None else _f32(bias).reshape(-1)
+        out = ctypes.c_void_p()
+        _check(lib().vh_prepare_conv2d_f32(self._h, in_c, out_c, kh, kw, stride, pad, _fp(w),
+                                           _fp(b) if b is not None else None, ctypes.byref(out)))
+        return Conv2d(self, out.value)
+
+    def conv2d_f32(self, x: Tensor, in_c, ih, iw, weight, out_c, kh, kw, stride, pad,
+                   bias=None) -> Tensor:
+        w = _f32(weight).reshape(-1)
+        b = None if bias is None else _f32(bias).reshape(-1)
+        return self._out(lib().vh_conv2d_f32, x.handle, in_c, ih, iw, _fp(w), out_c, kh, kw,
+                         stride, pad, _fp(b) if b is not None else None)
+
+    def prepare_conv_transpose2d_f32(self, in_c, out_c, kh, kw, stride, weight,
+                                     bias=None) -> ConvTranspose2d:
+        w = _f32(weight).reshape(-1)
+        b = None if bias is None else _f32(bias).reshape(-1)
+        out = ctypes.c_void_p()
+        _check(lib().vh_prepare_conv_transpose2d_f32(self._h, in_c, out_c, kh, kw, stride, _fp(w),
+                                                     _fp(b) if b is not None else None,
+                                                     ctypes.byref(out)))
+        return ConvTranspose2d(self, out.value)
+
+    def conv_transpose2d_f32(self, x: Tensor, in_c, ih, iw, weight, out_c, kh, kw, stride,
+                             bias=None) -> Tensor:
+        w = _f32(weight).reshape(-1)
+        b = None if bias is None else _f32(bias).reshape(-1)
+        return self._out(lib().vh_conv_transpose2d_f32, x.handle, in_c, ih, iw, _fp(w), out_c,
+                         kh, kw, stride, _fp(b) if b is not None else None)
+
+    def bilinear_resize_f32(self, x: Tensor, c, ih, iw, oh, ow) -> Tensor:
+        return self._out(lib().vh_bilinear_resize_f32, x.handle, c, ih, iw, oh, ow)
+
+    def bilinear_resize_align_corners_f32(self, x: Tensor, c, ih, iw, oh, ow,
+                                          add: Tensor | None = None) -> Tensor:
+        return self._out(lib().vh_bilinear_resize_align_corners_f32, x.handle, c, ih, iw, oh, ow,
+                         add.handle if add is not None else None)
 
     # -- DA3 block / encoder
     def prepare_block(self, weights: dict, q8_0: bool = False) -> Block:
