@@ -203,6 +203,97 @@ def gpu_elementwise(reps: int = 20) -> dict:
     return out
 
 
+def gpu_dpt(reps: int = 20) -> dict:
+    """DPT-head operations at DA3-BASE fusion shapes: a 3x3 convolution
+    128 -> 128 over the 144 x 96 map (a residual conv unit), the k4s4
+    transposed convolution 96 -> 96 from the 24 x 36 patch grid, and the
+    align-corners 2x upsample of 128 channels from 72 x 48.  Per-launch HIP
+    event timing; conv FLOPs are 2 * pixels * out_c * in_c * 9."""
+    import vestra_hip as vh
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    rt = vh.Runtime(0)
+    c, h, w = 128, 96, 144
+    x = rt.upload_f32(oracle.xorshift32_vec(1, c * h * w))
+    wt = oracle.xorshift32_vec(2, c * c * 9) * np.float32(1.0 / 34.0)
+    conv = rt.prepare_conv2d_f32(c, c, 3, 3, 1, 1, wt, oracle.xorshift32_vec(3, c))
+    tc, th, tw = 96, 24, 36
+    xt = rt.upload_f32(oracle.xorshift32_vec(4, tc * th * tw))
+    ct = rt.prepare_conv_transpose2d_f32(tc, tc, 4, 4, 4, oracle.xorshift32_vec(5, tc * tc * 16),
+                                         oracle.xorshift32_vec(6, tc))
+    rh, rw = 48, 72
+    xr = rt.upload_f32(oracle.xorshift32_vec(7, c * rh * rw))
+    for _ in range(3):
+        conv.run(x, h, w)
+        ct.run(xt, th, tw)
+        rt.bilinear_resize_align_corners_f32(xr, c, rh, rw, 2 * rh, 2 * rw)
+    rt.synchronize()
+    rt.profile_reset()
+    rt.profile_enable(True)
+    keep = []
+    for _ in range(reps):
+        keep.append(conv.run(x, h, w))
+        keep.append(ct.run(xt, th, tw))
+        keep.append(rt.bilinear_resize_align_corners_f32(xr, c, rh, rw, 2 * rh, 2 * rw))
+    prof = rt.profile_report()
+    rt.profile_enable(False)
+    del keep
+
+    def us(name, per=1):
+        n, ms = prof[name]
+        return 1e3 * ms / n * per
+
+    flops = 2.0 * h * w * c * c * 9
+    conv_parts = {"to_hwc": us("conv_to_hwc"), "im2col": us("im2col"), "gemm": us("conv_gemm"),
+                  "to_chw": us("conv_to_chw")}
+    conv_us = sum(conv_parts.values())
+    t_flops = 2.0 * th * tw * tc * tc * 16
+    t_parts = {"to_hwc": us("conv_transpose_to_hwc"), "gemm": us("conv_transpose_gemm"),
+               "scatter": us("patch_scatter")}
+    t_us = sum(t_parts.values())
+    r_us = us("bilinear_align_corners")
+    r_bytes = 4.0 * c * (rh * rw + 4 * rh * rw)
+    out = {
+        "conv3x3_128_144x96": {
+            "us": round(conv_us, 2), "parts_us": {k: round(v, 2) for k, v in conv_parts.items()},
+            "tflops": round(flops / (conv_us * 1e-6) / 1e12, 2),
+            "gemm_tflops": round(flops / (conv_parts["gemm"] * 1e-6) / 1e12, 2),
+            "frac_fp32_mfma": round(flops / (conv_us * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)},
+        "conv_transpose_k4s4_96_24x36": {
+            "us": round(t_us, 2), "parts_us": {k: round(v, 2) for k, v in t_parts.items()},
+            "tflops": round(t_flops / (t_us * 1e-6) / 1e12, 2)},
+        "resize_align_corners_128_48x72_to_96x144": {
+            "us": round(r_us, 2), "gbs": round(r_bytes / (r_us * 1e-6) / 1e9, 1),
+            "frac_hbm": round(r_bytes / (r_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)},
+    }
+    log(f"  dpt conv3x3 {conv_us:.2f} us ({out['conv3x3_128_144x96']['tflops']} TF/s), "
+        f"transposed conv {t_us:.2f} us, resize {r_us:.2f} us")
+    return out
+
+
+def cpu_dpt_conv(budget_s: float) -> dict:
+    """The oracle's direct conv2d (the crate's conv2d_naive restated, all
+    OpenMP threads) on the bench's 3x3 convolution shape."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    c, h, w = 128, 96, 144
+    x = oracle.xorshift32_vec(1, c * h * w)
+    wt = oracle.xorshift32_vec(2, c * c * 9) * np.float32(1.0 / 34.0)
+    b = oracle.xorshift32_vec(3, c)
+    times = []
+    start = time.perf_counter()
+    while (not times or time.perf_counter() - start < budget_s) and len(times) < 20:
+        t0 = time.perf_counter()
+        oracle.conv2d_naive(x, c, h, w, wt, c, 3, 3, 1, 1, b)
+        times.append(time.perf_counter() - t0)
+    return {"value": round(float(np.median(times)) * 1e6, 1), "unit": "us",
+            "cores": oracle.threads(), "kind": "port",
+            "sample": f"{len(times)} runs of conv2d_naive 128->128 3x3 at 144x96 (median)"}
+
+
 def cpu_block(budget_s: float) -> dict:
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
@@ -252,6 +343,7 @@ def main() -> int:
     q8 = gpu_q8_0(max(10, min(args.steps, 100)))
     q8_block = gpu_block(max(10, min(args.steps, 100)), args.warmup, q8_0=True)
     elementwise = gpu_elementwise()
+    dpt = gpu_dpt()
     if args.calibrate:
         import vestra_hip as vh
 
@@ -301,9 +393,11 @@ def main() -> int:
                        "us_per_block": round(q8_block["ms_per_step"] * 1e3, 2),
                        "kernels": q8_block["kernels"]},
         "elementwise_at_scale": elementwise,
+        "dpt": dpt,
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_block(args.cpu_seconds)
+        dpt["conv3x3_128_144x96"]["cpu_baseline"] = cpu_dpt_conv(5.0)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -12,6 +12,8 @@
 //
 // The resize kernels restate src/resample.rs op for op (separately rounded
 // f32 ops, the same coordinate formulas), so they are bit-exact.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -57,6 +59,34 @@ __global__ __launch_bounds__(256) void im2col_t_kernel(const float *__restrict__
         for (int r = 0; r < 16; r++) {
             const int pl = pr * 16 + r, p = p0 + pl;
             if (p < npix) col[(size_t)p * K + k] = tile[kl][pl];
+        }
+    }
+}
+
+// colT[p][(ky*kw + kx)*in_c + ic] from a channel-last input xh [ih*iw][in_c]
+// (in_c % 4 == 0): each tap of a pixel is one contiguous run of in_c values,
+// copied as float4, zeros where the tap falls in the padding.  One workgroup
+// walks whole pixels, so the writes of a row are contiguous.
+__global__ __launch_bounds__(256) void im2col_hwc_kernel(const float *__restrict__ xh,
+                                                         float *__restrict__ col, int in_c, int ih,
+                                                         int iw, int kh, int kw, int stride,
+                                                         int pad, int oh, int ow, int relu) {
+    const int c4n = in_c / 4, K4 = c4n * kh * kw, npix = oh * ow;
+    for (int p = blockIdx.x; p < npix; p += gridDim.x) {
+        const int oy = p / ow, ox = p % ow;
+        f32x4 *dst = reinterpret_cast<f32x4 *>(col + (size_t)p * K4 * 4);
+        for (int j = threadIdx.x; j < K4; j += blockDim.x) {
+            const int tap = j / c4n, c4 = j - tap * c4n;
+            const int iy = oy * stride + tap / kw - pad, ix = ox * stride + tap % kw - pad;
+            f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (iy >= 0 && iy < ih && ix >= 0 && ix < iw) {
+                v = reinterpret_cast<const f32x4 *>(xh + ((size_t)iy * iw + ix) * in_c)[c4];
+                if (relu) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[e] = fmaxf(v[e], 0.0f);
+                }
+            }
+            dst[j] = v;
         }
     }
 }
@@ -139,29 +169,35 @@ __device__ __forceinline__ Tap align_corners_tap(int dst, int len_in, int len_ou
     return Tap{i0, i1, frac};
 }
 
-// One thread per output element; top = r0[x0]*(1-fx) + r0[x1]*fx, the same
+// A thread owns one output position (oy, ox) of a group of channels: the two
+// taps are computed once (the row tap is uniform across the workgroup's row)
+// and reused for every channel.  top = r0[x0]*(1-fx) + r0[x1]*fx, the same
 // for the lower row, out = top*(1-fy) + bot*fy (+ add), as
 // src/resample.rs:72-76 rounds them.
+constexpr int kResizeChannels = 8;  // channels per thread
 template <bool ALIGN>
 __global__ __launch_bounds__(256) void bilinear_kernel(const float *__restrict__ in,
                                                        const float *__restrict__ add,
                                                        float *__restrict__ out, int c, int ih,
                                                        int iw, int oh, int ow, float scale_y,
                                                        float scale_x) {
-    const size_t total = (size_t)c * oh * ow;
-    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-         e += (size_t)gridDim.x * blockDim.x) {
-        const int ox = (int)(e % ow);
-        const size_t r = e / ow;
-        const int oy = (int)(r % oh), ch = (int)(r / oh);
-        const Tap ty = ALIGN ? align_corners_tap(oy, ih, oh) : half_pixel_tap(oy, scale_y, ih);
-        const Tap tx = ALIGN ? align_corners_tap(ox, iw, ow) : half_pixel_tap(ox, scale_x, iw);
-        const float *plane = in + (size_t)ch * ih * iw;
-        const float *row0 = plane + (size_t)ty.i0 * iw, *row1 = plane + (size_t)ty.i1 * iw;
-        const float gx = sub_rn(1.0f, tx.frac), gy = sub_rn(1.0f, ty.frac);
-        const float top = add_rn(mul_rn(row0[tx.i0], gx), mul_rn(row0[tx.i1], tx.frac));
-        const float bot = add_rn(mul_rn(row1[tx.i0], gx), mul_rn(row1[tx.i1], tx.frac));
+    const int ox = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int oy = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (ox >= ow || oy >= oh) return;
+    const Tap ty = ALIGN ? align_corners_tap(oy, ih, oh) : half_pixel_tap(oy, scale_y, ih);
+    const Tap tx = ALIGN ? align_corners_tap(ox, iw, ow) : half_pixel_tap(ox, scale_x, iw);
+    const float gx = sub_rn(1.0f, tx.frac), gy = sub_rn(1.0f, ty.frac);
+    const size_t in_plane = (size_t)ih * iw, out_plane = (size_t)oh * ow;
+    const size_t o00 = (size_t)ty.i0 * iw + tx.i0, o01 = (size_t)ty.i0 * iw + tx.i1;
+    const size_t o10 = (size_t)ty.i1 * iw + tx.i0, o11 = (size_t)ty.i1 * iw + tx.i1;
+    const size_t opos = (size_t)oy * ow + ox;
+    const int c0 = blockIdx.z * kResizeChannels, c1 = min(c, c0 + kResizeChannels);
+    for (int ch = c0; ch < c1; ch++) {
+        const float *plane = in + (size_t)ch * in_plane;
+        const float top = add_rn(mul_rn(plane[o00], gx), mul_rn(plane[o01], tx.frac));
+        const float bot = add_rn(mul_rn(plane[o10], gx), mul_rn(plane[o11], tx.frac));
         float v = add_rn(mul_rn(top, gy), mul_rn(bot, ty.frac));
+        const size_t e = (size_t)ch * out_plane + opos;
         if (add) v = add_rn(v, add[e]);
         out[e] = v;
     }
@@ -192,6 +228,19 @@ hipError_t launch_im2col_t(hipStream_t s, const float *in, float *col, size_t in
     return hipGetLastError();
 }
 
+hipError_t launch_im2col_hwc(hipStream_t s, const float *xh, float *col, size_t in_c, size_t ih,
+                             size_t iw, size_t kh, size_t kw, size_t stride, size_t pad,
+                             size_t oh, size_t ow, bool relu) {
+    const size_t npix = oh * ow;
+    if (npix == 0 || in_c == 0) return hipSuccess;
+    if (in_c % 4 != 0) return hipErrorInvalidValue;
+    const unsigned blocks = (unsigned)std::min<size_t>(npix, 65536);
+    im2col_hwc_kernel<<<blocks, 256, 0, s>>>(xh, col, (int)in_c, (int)ih, (int)iw, (int)kh,
+                                             (int)kw, (int)stride, (int)pad, (int)oh, (int)ow,
+                                             relu ? 1 : 0);
+    return hipGetLastError();
+}
+
 hipError_t launch_patch_scatter(hipStream_t s, const float *c, float *out, size_t out_c,
                                 size_t ih, size_t iw, size_t kh, size_t kw) {
     const size_t total = out_c * ih * kh * iw * kw;
@@ -217,16 +266,18 @@ hipError_t launch_bilinear(hipStream_t s, const float *in, const float *add, flo
                            bool align_corners) {
     const size_t total = c * oh * ow;
     if (total == 0 || ih == 0 || iw == 0) return hipSuccess;
+    const dim3 grid((unsigned)((ow + 63) / 64), (unsigned)((oh + 3) / 4),
+                    (unsigned)((c + kResizeChannels - 1) / kResizeChannels));
+    if (grid.y > 65535 || grid.z > 65535) return hipErrorInvalidValue;
     if (align_corners) {
-        bilinear_kernel<true><<<grid_for(total), 256, 0, s>>>(in, add, out, (int)c, (int)ih,
-                                                              (int)iw, (int)oh, (int)ow, 0.0f,
-                                                              0.0f);
+        bilinear_kernel<true><<<grid, 256, 0, s>>>(in, add, out, (int)c, (int)ih, (int)iw,
+                                                   (int)oh, (int)ow, 0.0f, 0.0f);
     } else {
         // scale = len_in / len_out in f32 (src/resample.rs:26-27), correctly
         // rounded on the host.
         const float sy = (float)ih / (float)oh, sx = (float)iw / (float)ow;
-        bilinear_kernel<false><<<grid_for(total), 256, 0, s>>>(in, add, out, (int)c, (int)ih,
-                                                               (int)iw, (int)oh, (int)ow, sy, sx);
+        bilinear_kernel<false><<<grid, 256, 0, s>>>(in, add, out, (int)c, (int)ih, (int)iw,
+                                                    (int)oh, (int)ow, sy, sx);
     }
     return hipGetLastError();
 }

@@ -65,6 +65,11 @@ hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k,
 hipError_t launch_im2col_t(hipStream_t s, const float *in, float *col, size_t in_c, size_t ih,
                            size_t iw, size_t kh, size_t kw, size_t stride, size_t pad, size_t oh,
                            size_t ow, bool relu);
+// colT [oh*ow][kh*kw*in_c] from a channel-last input xh [ih*iw][in_c]
+// (in_c % 4 == 0), k ordered (ky, kx, ic); ReLU on the input when relu.
+hipError_t launch_im2col_hwc(hipStream_t s, const float *xh, float *col, size_t in_c, size_t ih,
+                             size_t iw, size_t kh, size_t kw, size_t stride, size_t pad,
+                             size_t oh, size_t ow, bool relu);
 // c [ih*iw][out_c*kh*kw] -> out [out_c][ih*kh][iw*kw] (kernel == stride).
 hipError_t launch_patch_scatter(hipStream_t s, const float *c, float *out, size_t out_c,
                                 size_t ih, size_t iw, size_t kh, size_t kw);

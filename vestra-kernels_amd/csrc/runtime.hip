@@ -1850,7 +1850,10 @@ extern "C" vh_status vh_encoder_run(const vh_runtime *rt, const vh_block *const 
 struct vh_conv2d {
     Rt rt;
     size_t in_c = 0, out_c = 0, kh = 0, kw = 0, stride = 0, pad = 0;
-    float *w = nullptr;     // OIHW = [out_c][in_c*kh*kw], the GEMM's Bt operand
+    // in_c % 4 == 0: weight [out_c][kh][kw][in_c] and channel-last patches;
+    // else OIHW = [out_c][in_c*kh*kw].  Either is the GEMM's Bt operand.
+    bool hwc = false;
+    float *w = nullptr;
     float *bias = nullptr;  // [out_c] or null
     ~vh_conv2d() {
         if (!rt) return;
@@ -1906,24 +1909,36 @@ vh_status conv_run(RtState &s, const vh_conv2d &c, const float *in, size_t ih, s
     const size_t oh = (ih + 2 * c.pad - c.kh) / c.stride + 1;
     const size_t ow = (iw + 2 * c.pad - c.kw) / c.stride + 1;
     const size_t npix = oh * ow, K = c.in_c * c.kh * c.kw;
-    float *col = nullptr, *tmp = nullptr;
-    vh_status st = dalloc(s, npix * K, &col, "convolution patch allocation");
+    const bool plain = c.kh == 1 && c.kw == 1 && c.stride == 1 && c.pad == 0 && !relu;
+    float *xh = nullptr, *col = nullptr, *tmp = nullptr;
+    vh_status st = VH_OK;
+    if (c.hwc && !plain) {
+        // Channel-last copy of the input, then one contiguous run per tap.
+        st = dalloc(s, ih * iw * c.in_c, &xh, "convolution staging allocation");
+        if (!st)
+            st = launch(s, "conv_to_hwc", [&] {
+                return vh::launch_transpose(s.stream, in, xh, c.in_c, ih * iw);
+            });
+    }
+    if (!st) st = dalloc(s, npix * K, &col, "convolution patch allocation");
     if (!st) st = dalloc(s, npix * c.out_c, &tmp, "convolution output allocation");
     if (!st) {
-        const bool plain = c.kh == 1 && c.kw == 1 && c.stride == 1 && c.pad == 0 && !relu;
-        st = launch(s, plain ? "transpose" : "im2col", [&] {
-            return plain ? vh::launch_transpose(s.stream, in, col, c.in_c, npix)
-                         : vh::launch_im2col_t(s.stream, in, col, c.in_c, ih, iw, c.kh, c.kw,
-                                               c.stride, c.pad, oh, ow, relu);
+        st = launch(s, plain ? "conv_to_hwc" : "im2col", [&] {
+            if (plain) return vh::launch_transpose(s.stream, in, col, c.in_c, npix);
+            if (c.hwc)
+                return vh::launch_im2col_hwc(s.stream, xh, col, c.in_c, ih, iw, c.kh, c.kw,
+                                             c.stride, c.pad, oh, ow, relu);
+            return vh::launch_im2col_t(s.stream, in, col, c.in_c, ih, iw, c.kh, c.kw, c.stride,
+                                       c.pad, oh, ow, relu);
         });
     }
     if (!st) st = gemm_nt(s, col, c.w, c.bias, tmp, npix, c.out_c, K, "conv_gemm");
     if (!st)
-        st = launch(s, "transpose", [&] {
+        st = launch(s, "conv_to_chw", [&] {
             return vh::launch_transpose(s.stream, tmp, out, npix, c.out_c);
         });
-    if (col) hipFreeAsync(col, s.stream);
-    if (tmp) hipFreeAsync(tmp, s.stream);
+    for (float *p : {xh, col, tmp})
+        if (p) hipFreeAsync(p, s.stream);
     return st;
 }
 
@@ -1968,7 +1983,20 @@ vh_status prepare_conv(const vh_runtime *rt, size_t in_c, size_t out_c, size_t k
     c->kw = kw;
     c->stride = stride;
     c->pad = pad;
-    vh_status st = upload_array(s, weight, n, &c->w, "conv2d weight upload");
+    c->hwc = in_c % 4 == 0;
+    vh_status st;
+    if (c->hwc) {
+        // OIHW -> [out_c][kh][kw][in_c], the k order of the channel-last patches.
+        std::vector<float> packed(n);
+        const size_t taps = kh * kw;
+        for (size_t o = 0; o < out_c; o++)
+            for (size_t i = 0; i < in_c; i++)
+                for (size_t t = 0; t < taps; t++)
+                    packed[(o * taps + t) * in_c + i] = weight[(o * in_c + i) * taps + t];
+        st = upload_array(s, packed.data(), n, &c->w, "conv2d weight upload");
+    } else {
+        st = upload_array(s, weight, n, &c->w, "conv2d weight upload");
+    }
     if (!st && bias) st = upload_array(s, bias, out_c, &c->bias, "conv2d bias upload");
     if (st) {
         delete c;
@@ -2078,7 +2106,7 @@ vh_status conv_t_new(const vh_conv_transpose2d *c, const vh_tensor *input, size_
         st = dalloc(s, plane * c->in_c, &xt, "conv_transpose2d staging allocation");
         if (!st) st = dalloc(s, plane * cols, &tmp, "conv_transpose2d staging allocation");
         if (!st)
-            st = launch(s, "transpose", [&] {
+            st = launch(s, "conv_transpose_to_hwc", [&] {
                 return vh::launch_transpose(s.stream, input->ptr, xt, c->in_c, plane);
             });
         if (!st) st = gemm_nt(s, xt, c->w, c->bias_x, tmp, plane, cols, c->in_c, "conv_transpose_gemm");
@@ -2116,8 +2144,9 @@ vh_status resize_new(const vh_runtime *rt, const vh_tensor *input, size_t c, siz
         return fail(VH_ERR_KERNEL, std::string(name) + ": size overflows");
     TRY(check_tensor_len(input, ilen, name));
     if (add) TRY(check_tensor_len(add, olen, name));
-    if (c > INT32_MAX || ih > INT32_MAX || iw > INT32_MAX || oh > INT32_MAX || ow > INT32_MAX)
-        return fail(VH_ERR_KERNEL, std::string(name) + ": dimension exceeds 2^31-1");
+    if (c > INT32_MAX || ih > INT32_MAX || iw > INT32_MAX || oh > INT32_MAX || ow > INT32_MAX ||
+        (oh + 3) / 4 > 65535 || (c + 7) / 8 > 65535)
+        return fail(VH_ERR_KERNEL, std::string(name) + ": shape exceeds the launch grid");
     GUARD_BEGIN
     RtState &s = *rt->s;
     TRY(set_device(s));
