@@ -159,47 +159,67 @@ def gpu_q8_0(steps: int) -> dict:
 
 
 def gpu_elementwise(reps: int = 20) -> dict:
-    """The bandwidth-bound kernels at sizes where bandwidth, not launch
-    latency, decides: LayerNorm over 4 x 865 tokens, GELU over the batched
-    fc1 output, and the residual add over 16 Mi floats.  Per-launch HIP
-    event timing; bytes are the algorithmic reads plus writes."""
+    """The bandwidth-bound kernels, per-launch HIP event timing, bytes = the
+    algorithmic reads plus writes.  Two size classes: the encoder's own shapes
+    (LayerNorm and quantisation over 4 x 865 tokens, GELU over the batched fc1
+    output), and sizes where bandwidth rather than launch and first-load
+    latency decides (16-33 Mi floats)."""
     import vestra_hip as vh
-    from vestra_hip import seeded
+    from vestra_hip import da3, seeded
 
     rt = vh.Runtime(0)
-    rows = 4 * T
-    x = rt.upload_f32(seeded.normal(31, rows * D))
     g = rt.upload_f32(np.ones(D, np.float32))
     b = rt.upload_f32(np.zeros(D, np.float32))
-    f = rt.upload_f32(seeded.normal(32, rows * F))
-    n_add = 16 * 1024 * 1024
-    a1 = rt.upload_f32(np.ones(n_add, np.float32))
-    a2 = rt.upload_f32(np.ones(n_add, np.float32))
-    for _ in range(3):
-        rt.layernorm_f32(x, g, b, rows, D, 1e-6)
-        rt.gelu_f32_in_place(f)
-        rt.add_f32_in_place(a1, a2)
-    rt.synchronize()
-    rt.profile_reset()
-    rt.profile_enable(True)
-    keep = []
-    for _ in range(reps):
-        keep.append(rt.layernorm_f32(x, g, b, rows, D, 1e-6))
-        rt.gelu_f32_in_place(f)
-        rt.add_f32_in_place(a1, a2)
-    prof = rt.profile_report()
-    rt.profile_enable(False)
-    del keep
-    sizes = {"layernorm": (2 * rows * D * 4 + 2 * D * 4, f"{rows}x{D}"),
-             "gelu": (2 * rows * F * 4, f"{rows}x{F}"),
-             "add": (3 * n_add * 4, f"{n_add}")}
+    cases = []
+
+    def ln_case(rows):
+        x = rt.upload_f32(seeded.normal(31, rows * D))
+        return (f"layernorm {rows}x{D}", lambda: rt.layernorm_f32(x, g, b, rows, D, 1e-6),
+                2 * rows * D * 4 + 2 * D * 4, "layernorm")
+
+    def gelu_case(n):
+        f = rt.upload_f32(seeded.normal(32, n))
+        return (f"gelu {n}", lambda: rt.gelu_f32_in_place(f), 2 * n * 4, "gelu")
+
+    def add_case(n):
+        a1, a2 = rt.upload_f32(np.ones(n, np.float32)), rt.upload_f32(np.ones(n, np.float32))
+        return (f"add {n}", lambda: rt.add_f32_in_place(a1, a2), 3 * n * 4, "add")
+
+    def q8_case(rows):
+        x = rt.upload_f32(seeded.normal(33, rows * D))
+        return (f"quantize_q8_0 {rows}x{D}", lambda: rt.quantize_q8_0(x, rows, D),
+                rows * D * 4 + rows * D + rows * D // 16, "quantize_q8_0")
+
+    def rope_case(heads, grid_h, grid_w):
+        n = grid_h * grid_w + 1
+        x = rt.upload_f32(seeded.normal(34, heads * n * HD))
+        pos = da3.positions_yx(grid_h, grid_w)
+        return (f"rope2d {heads}x{n}x{HD}",
+                lambda: rt.rope2d_f32_in_place(x, heads, n, HD, pos, da3.ROPE_FREQ),
+                2 * heads * n * HD * 4, "rope2d")
+
+    block_shapes = [ln_case(4 * T), gelu_case(4 * T * F), q8_case(4 * T), rope_case(2 * 4 * H, 24, 36)]
+    at_scale = [ln_case(21845), gelu_case(32 * 1024 * 1024), add_case(32 * 1024 * 1024),
+                q8_case(21845), rope_case(2 * 4 * H, 72, 48)]
     out = {}
-    for name, (nbytes, shape) in sizes.items():
-        us = 1e3 * prof[name][1] / prof[name][0]
-        gbs = nbytes / (us * 1e-6) / 1e9
-        out[name] = {"shape": shape, "us": round(us, 2), "gbs": round(gbs, 1),
-                     "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
-        log(f"  {name:10s} {shape:>10s} {us:8.2f} us {gbs:8.1f} GB/s")
+    for label, cases in (("block_shapes", block_shapes), ("bandwidth_sizes", at_scale)):
+        res = {}
+        for name, fn, nbytes, prof_name in cases:
+            for _ in range(3):
+                fn()
+            rt.synchronize()
+            rt.profile_reset()
+            rt.profile_enable(True)
+            keep = [fn() for _ in range(reps)]
+            prof = rt.profile_report()
+            rt.profile_enable(False)
+            del keep
+            us = 1e3 * prof[prof_name][1] / prof[prof_name][0]
+            gbs = nbytes / (us * 1e-6) / 1e9
+            res[name] = {"us": round(us, 2), "gbs": round(gbs, 1),
+                         "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes}
+            log(f"  {name:28s} {us:8.2f} us {gbs:8.1f} GB/s")
+        out[label] = res
     return out
 
 

@@ -317,6 +317,12 @@ def test_rope2d_bit_exact_with_host_table(rt):
     t2 = rt.upload_f32(x2)
     rt.rope2d_f32_in_place(t2, 3, 7, 16, pos2, 100.0)
     assert_bits_equal(rt.download_f32(t2), O.rope2d(x2, 3, 7, 16, pos2, 100.0), "rope2d small")
+    # head_dim 64 with a row count that leaves idle lanes in the last workgroup
+    x3 = seeded.normal(72, 3 * 97 * 64)
+    pos3 = np.array([[i % 5, i // 5] for i in range(97)], np.int64).reshape(-1)
+    t3 = rt.upload_f32(x3)
+    rt.rope2d_f32_in_place(t3, 3, 97, 64, pos3, 100.0)
+    assert_bits_equal(rt.download_f32(t3), O.rope2d(x3, 3, 97, 64, pos3, 100.0), "rope2d ragged")
 
 
 def test_qk_norm_rope_production_shape(rt):

@@ -232,6 +232,34 @@ __global__ void rope2d_kernel(float *__restrict__ x, size_t heads, size_t n, siz
     }
 }
 
+// rope2d for head_dim 64 (the DA3 shape), the same arithmetic as
+// rope2d_kernel: 16 lanes per 64-wide row, lane j holding dims 4j..4j+3
+// (axis j / 8); the rotation partner (dim +/- 16) lives in lane j ^ 4.
+// Rows are contiguous, so a wave reads and writes 1 KB at a time, and the
+// [n][2][16][sin, cos] table is read as two float4 per lane.
+__global__ __launch_bounds__(256) void rope2d_hd64_kernel(float *__restrict__ x, int rows, int n,
+                                                          const float *__restrict__ rot) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    const int row = min(t >> 4, rows - 1);  // idle lanes shadow the last row
+    const int j = t & 15;
+    f32x4 *p = reinterpret_cast<f32x4 *>(x + (size_t)row * 64) + j;
+    const f32x4 v = *p;
+    f32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; e++) w[e] = __shfl_xor(v[e], 4, 16);
+    const int pos = row % n, axis = j >> 3, q4 = (j & 3) * 4;
+    const f32x4 *rp = reinterpret_cast<const f32x4 *>(rot + (((size_t)pos * 2 + axis) * 16 + q4) * 2);
+    const f32x4 r0 = rp[0], r1 = rp[1];  // (sin, cos) of dims q4 .. q4 + 3
+    const float sn[4] = {r0[0], r0[2], r1[0], r1[2]}, cs[4] = {r0[1], r0[3], r1[1], r1[3]};
+    const bool first = (j & 4) == 0;  // holds the a values of (a, b) = (dim, dim + 16)
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        o[e] = first ? sub_rn(mul_rn(v[e], cs[e]), mul_rn(w[e], sn[e]))
+                     : add_rn(mul_rn(v[e], cs[e]), mul_rn(w[e], sn[e]));
+    if ((t >> 4) < rows) *p = o;
+}
+
 // qk_norm_rope (src/specialized.rs:412-454): 16 lanes per 64-wide row, lane j
 // holds dims 4j..4j+3; the rotation partner (dim + 16) lives in lane j ^ 4.
 // LayerNorm sums use a 16-lane tree (tolerance-checked against the CPU order).
@@ -406,6 +434,12 @@ hipError_t launch_rope2d(hipStream_t s, float *x, size_t heads, size_t n, size_t
                          const float *rot) {
     size_t pairs = heads * n * (head_dim / 2);
     if (pairs == 0) return hipSuccess;
+    const size_t rows = heads * n;
+    if (head_dim == 64 && rows <= (size_t)INT32_MAX / 16) {
+        rope2d_hd64_kernel<<<(unsigned)((rows * 16 + 255) / 256), 256, 0, s>>>(x, (int)rows, (int)n,
+                                                                               rot);
+        return hipGetLastError();
+    }
     rope2d_kernel<<<grid_for(pairs), kThreads, 0, s>>>(x, heads, n, head_dim, rot);
     return hipGetLastError();
 }

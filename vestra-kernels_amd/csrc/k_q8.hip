@@ -27,33 +27,39 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
-// quantize_row_q8_0 (src/q8_0_dot.rs:27-46): eight lanes per 32-value block,
-// four values each; amax is a max (order-free) over the eight lanes.  Block b
-// of the row-major input (row b / nbr, k-slice b % nbr) is stored block-major.
+// quantize_row_q8_0 (src/q8_0_dot.rs:27-46): four lanes per 32-value block,
+// eight values each; amax is a max (order-free) over the four lanes, taken
+// with two DPP quad permutations (lane ^ 1, lane ^ 2).  Lane groups walk the
+// block-major output slots in order (slot j * rows + r holds row r's k-slice
+// j), so a wave writes 512 contiguous bytes of values and 32 of scales and
+// reads sixteen 128-byte row segments.  A 2-D grid (x: rows, y: k-slices)
+// keeps the slot arithmetic free of 64-bit division.
 __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x,
                                                             int8_t *__restrict__ qs,
                                                             uint16_t *__restrict__ dbits,
-                                                            size_t nblocks, size_t rows,
-                                                            size_t nbr) {
-    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t b = t >> 3;
-    const int part = (int)(t & 7);
-    const bool live = b < nblocks;
-    const size_t bb = live ? b : nblocks - 1;  // idle lanes shadow the last block
-    const size_t dst = (bb % nbr) * rows + bb / nbr;  // block-major index
-    const f32x4 v = reinterpret_cast<const f32x4 *>(x + bb * 32)[part];
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+                                                            int rows, int nbr) {
+    // blockIdx.y is the k-slice j; the threads of x walk its rows.
+    const int j = blockIdx.y;
+    const int r0 = (blockIdx.x * blockDim.x + threadIdx.x) >> 2;
+    const int part = threadIdx.x & 3;
+    const bool live = r0 < rows;
+    const int r = live ? r0 : rows - 1;  // idle lanes shadow the last row
+    const size_t dst = (size_t)j * rows + r;  // block-major slot
+    const size_t bb = (size_t)r * nbr + j;    // row-major block
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(x + bb * 32) + 2 * part;
+    const f32x4 v0 = src[0], v1 = src[1];
+    float amax = fmaxf(fmaxf(fmaxf(fabsf(v0[0]), fabsf(v0[1])), fmaxf(fabsf(v0[2]), fabsf(v0[3]))),
+                       fmaxf(fmaxf(fabsf(v1[0]), fabsf(v1[1])), fmaxf(fabsf(v1[2]), fabsf(v1[3]))));
+    amax = fmaxf(amax, dpp_f32<0xb1>(amax));
+    amax = fmaxf(amax, dpp_f32<0x4e>(amax));
     const float d = div_rn(amax, 127.0f);
     const float inv = d != 0.0f ? div_rn(1.0f, d) : 0.0f;
     if (!live) return;
     if (part == 0) dbits[dst] = __builtin_bit_cast(uint16_t, (_Float16)d);
-    uint32_t w = 0;
+    uint32_t w[2] = {0, 0};
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        float q = roundf(mul_rn(v[e], inv));  // f32::round: half away from zero
+    for (int e = 0; e < 8; e++) {
+        float q = roundf(mul_rn(e < 4 ? v0[e] : v1[e - 4], inv));  // f32::round: half away from zero
         int qi;
         if (isnan(q)) {
             qi = 0;  // `NaN as i8` saturates to 0
@@ -61,9 +67,9 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
             q = fminf(fmaxf(q, -127.0f), 127.0f);
             qi = (int)q;
         }
-        w |= ((uint32_t)(qi & 0xff)) << (8 * e);
+        w[e >> 2] |= ((uint32_t)(qi & 0xff)) << (8 * (e & 3));
     }
-    reinterpret_cast<uint32_t *>(qs + dst * 32)[part] = w;
+    reinterpret_cast<uint2 *>(qs + dst * 32)[part] = make_uint2(w[0], w[1]);
 }
 
 // 256 threads = 4 waves in a 2x2 arrangement; each wave owns FM x FN MFMA
@@ -325,8 +331,9 @@ hipError_t launch_quantize_q8_0(hipStream_t s, const float *x, int8_t *qs, uint1
                                 size_t rows, size_t k) {
     size_t nblocks = rows * (k / 32);
     if (nblocks == 0) return hipSuccess;
-    quantize_q8_0_kernel<<<(unsigned)((nblocks * 8 + 255) / 256), 256, 0, s>>>(x, qs, d, nblocks, rows,
-                                                                             k / 32);
+    if (rows > (size_t)INT32_MAX / 4 || k / 32 > 65535) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((rows * 4 + 255) / 256), (unsigned)(k / 32));
+    quantize_q8_0_kernel<<<grid, 256, 0, s>>>(x, qs, d, (int)rows, (int)(k / 32));
     return hipGetLastError();
 }
 
