@@ -121,6 +121,32 @@ def gpu_block(steps: int, warmup: int, q8_0: bool = False) -> dict:
     return {"ms_per_step": total_ms / steps, "kernels": kernels}
 
 
+def gpu_encoder(reps: int = 5) -> dict:
+    """the 12-layer DA3-BASE encoder (independent seeded
+    layers) at 4 images x 865 tokens and at one 1008 x 672 image (3457
+    tokens), whole encoder between two HIP events."""
+    import vestra_hip as vh
+    from vestra_hip import da3, seeded
+
+    rt = vh.Runtime(0)
+    blocks = [rt.prepare_block(da3.block_weights(seed=50, layer=l)) for l in range(12)]
+    out = {}
+    for name, images, gh, gw in (("encoder_12x_4x865", 4, 24, 36), ("encoder_12x_1x3457", 1, 48, 72)):
+        tokens = gh * gw + 1
+        pos = da3.positions_yx(gh, gw)
+        x = rt.upload_f32(seeded.normal(51, images * tokens * D))
+        rt.encoder_run(blocks, x, images, tokens, pos)
+        rt.synchronize()
+        rt.timer_start()
+        for _ in range(reps):
+            rt.encoder_run(blocks, x, images, tokens, pos)
+        ms = rt.timer_stop() / reps
+        out[name] = {"images": images, "tokens": tokens, "layers": 12, "ms": round(ms, 3),
+                     "tokens_per_s": round(images * tokens / (ms * 1e-3), 1)}
+        log(f"  {name}: {ms:.3f} ms")
+    return out
+
+
 def gpu_q8_0(steps: int) -> dict:
     """fc1-shaped Q8_0 path.  X [865, 768] ~ N(0,1)
     quantised on the device each step, W [768, 3072] ~ N(0, 0.02^2)
@@ -364,6 +390,7 @@ def main() -> int:
     q8_block = gpu_block(max(10, min(args.steps, 100)), args.warmup, q8_0=True)
     elementwise = gpu_elementwise()
     dpt = gpu_dpt()
+    encoder = gpu_encoder()
     if args.calibrate:
         import vestra_hip as vh
 
@@ -414,6 +441,7 @@ def main() -> int:
                        "kernels": q8_block["kernels"]},
         "elementwise_at_scale": elementwise,
         "dpt": dpt,
+        "encoder": encoder,
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_block(args.cpu_seconds)
