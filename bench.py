@@ -292,8 +292,8 @@ def gpu_dpt(reps: int = 20) -> dict:
         return 1e3 * ms / n * per
 
     flops = 2.0 * h * w * c * c * 9
-    conv_parts = {"to_hwc": us("conv_to_hwc"), "im2col": us("im2col"), "gemm": us("conv_gemm"),
-                  "to_chw": us("conv_to_chw")}
+    conv_parts = {k: us(k) for k in ("conv_to_padded_hwc", "conv_to_hwc", "im2col", "conv_gemm",
+                                     "conv_to_chw") if k in prof}
     conv_us = sum(conv_parts.values())
     t_flops = 2.0 * th * tw * tc * tc * 16
     t_parts = {"to_hwc": us("conv_transpose_to_hwc"), "gemm": us("conv_transpose_gemm"),
@@ -305,7 +305,7 @@ def gpu_dpt(reps: int = 20) -> dict:
         "conv3x3_128_144x96": {
             "us": round(conv_us, 2), "parts_us": {k: round(v, 2) for k, v in conv_parts.items()},
             "tflops": round(flops / (conv_us * 1e-6) / 1e12, 2),
-            "gemm_tflops": round(flops / (conv_parts["gemm"] * 1e-6) / 1e12, 2),
+            "gemm_tflops": round(flops / (conv_parts["conv_gemm"] * 1e-6) / 1e12, 2),
             "frac_fp32_mfma": round(flops / (conv_us * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)},
         "conv_transpose_k4s4_96_24x36": {
             "us": round(t_us, 2), "parts_us": {k: round(v, 2) for k, v in t_parts.items()},

@@ -37,6 +37,10 @@ struct EpiArgs {
     const float *rot;
     size_t tail_start;
     float *partial;  // split-K: raw partial tiles [split][M][N]
+    // Implicit convolution (CONV kernels): A is a zero-padded channel-last
+    // image [rows][conv_in_c] and row m of the GEMM's A for k-slice k0 is
+    // image row m + (ky * conv_wp + kx), tap = k0 / conv_in_c = ky * conv_kw + kx.
+    int conv_in_c, conv_kw, conv_wp;
 };
 
 // Applies a Store / Gelu / Residual epilogue to one output element.
@@ -93,7 +97,10 @@ __device__ __forceinline__ void tile_of_block(bool xcd_order, int &tm, int &tn, 
 // or columns past the edge are never stored.  Selecting on the loaded value
 // would make the compiler wait for the prefetch before the MFMAs of the
 // current slice, so the load path stays select-free.
-template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT>
+// CONV (EXACT only): the A rows of a k-slice are the padded image rows of
+// one convolution tap, shifted by that tap's offset (see EpiArgs); conv_in_c
+// is a multiple of BK, so a slice never straddles two taps.
+template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, bool CONV = false>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__restrict__ A,
                                                               const float *__restrict__ Bt,
                                                               int M, int N, int K,
@@ -128,12 +135,24 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
 
     f32x4 ra[ACH], rb[BCH];
     auto gload = [&](int k0) {
-        if constexpr (EXACT) {
+        if constexpr (EXACT && CONV) {
+            const int tap = k0 / ep.conv_in_c;
+            const int shift = (tap / ep.conv_kw) * ep.conv_wp + tap % ep.conv_kw;
+            const int kin = k0 - tap * ep.conv_in_c;
+#pragma unroll
+            for (int i = 0; i < ACH; i++) {
+                int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
+                ra[i] = *reinterpret_cast<const f32x4 *>(
+                    A + ((size_t)min(m0 + row, M - 1) + shift) * ep.conv_in_c + kin + kq);
+            }
+        } else if constexpr (EXACT) {
 #pragma unroll
             for (int i = 0; i < ACH; i++) {
                 int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
                 ra[i] = *reinterpret_cast<const f32x4 *>(A + (size_t)min(m0 + row, M - 1) * K + k0 + kq);
             }
+        }
+        if constexpr (EXACT) {
 #pragma unroll
             for (int i = 0; i < BCH; i++) {
                 int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
@@ -524,10 +543,10 @@ struct Tile {
     int bm, bn, bk, wm, wn;
 };
 
-template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT>
+template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, bool CONV = false>
 hipError_t launch_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int splits, int kps) {
     constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 4) * sizeof(float);
-    auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, SPLIT, EXACT>;
+    auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, SPLIT, EXACT, CONV>;
     static bool configured = false;
     if (!configured) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
@@ -651,6 +670,26 @@ hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     }
 }
 
+// Implicit convolution: Store epilogue, whole slices, no K split.  The tile
+// comes from the per-shape table; its BK must divide the channel count.
+hipError_t dispatch_conv(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
+    Tile t;
+    int splits;
+    if (!tile_override(&t, &splits)) default_tile(g, &t, &splits);
+    if (g.conv_in_c % t.bk != 0) t = Tile{64, 64, 32, 2, 2};
+    if (g.conv_in_c % t.bk != 0 || g.k % t.bk != 0 || g.k == 0) return hipErrorInvalidValue;
+    const int kps = (int)g.k;
+#define VH_CONV_TILE(BM, BN, BK, WM, WN)                                                    \
+    if (t.bm == BM && t.bn == BN && t.bk == BK && t.wm == WM && t.wn == WN)                 \
+        return launch_tile<BM, BN, BK, WM, WN, Epi::Store, false, true, true>(s, g, ep, 1, kps);
+    VH_CONV_TILE(64, 64, 32, 2, 2)
+    VH_CONV_TILE(128, 128, 32, 2, 4)
+    VH_CONV_TILE(64, 128, 64, 2, 4)
+    VH_CONV_TILE(64, 128, 32, 2, 4)
+#undef VH_CONV_TILE
+    return launch_tile<64, 64, 32, 2, 2, Epi::Store, false, true, true>(s, g, ep, 1, kps);
+}
+
 }  // namespace
 
 // Residual GEMM followed by the LayerNorm of the updated rows: split K and
@@ -704,6 +743,13 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs &g) {
     ep.rot = g.rot;
     size_t total = g.m * g.n;
     ep.tail_start = total - total % 16;
+    if (g.conv_in_c) {
+        if (g.epi != Epi::Store) return hipErrorInvalidValue;
+        ep.conv_in_c = (int)g.conv_in_c;
+        ep.conv_kw = (int)g.conv_kw;
+        ep.conv_wp = (int)g.conv_wp;
+        return dispatch_conv(s, g, ep);
+    }
     switch (g.epi) {
         case Epi::Store: return dispatch<Epi::Store>(s, g, ep);
         case Epi::Gelu: return dispatch<Epi::Gelu>(s, g, ep);

@@ -1912,6 +1912,42 @@ vh_status conv_run(RtState &s, const vh_conv2d &c, const float *in, size_t ih, s
     const bool plain = c.kh == 1 && c.kw == 1 && c.stride == 1 && c.pad == 0 && !relu;
     float *xh = nullptr, *col = nullptr, *tmp = nullptr;
     vh_status st = VH_OK;
+    if (c.hwc && c.stride == 1 && c.in_c % 32 == 0 && !plain) {
+        // Implicit GEMM: the GEMM reads each tap's rows straight from the
+        // zero-padded channel-last image and computes the outputs on the
+        // padded grid (wp - ow junk columns per row, dropped at the end).
+        const size_t wp = iw + 2 * c.pad, hp = ih + 2 * c.pad;
+        const size_t rows = hp * wp + c.kw - 1, m = oh * wp;
+        st = dalloc(s, rows * c.in_c, &xh, "convolution staging allocation");
+        if (!st) st = dalloc(s, m * c.out_c, &tmp, "convolution output allocation");
+        if (!st)
+            st = launch(s, "conv_to_padded_hwc", [&] {
+                return vh::launch_chw_to_padded_hwc(s.stream, in, xh, c.in_c, ih, iw, c.pad, rows,
+                                                    relu);
+            });
+        if (!st) {
+            vh::GemmArgs g{};
+            g.a = xh;
+            g.bt = c.w;
+            g.m = m;
+            g.n = c.out_c;
+            g.k = K;
+            g.epi = vh::Epi::Store;
+            g.c = tmp;
+            g.bias = c.bias;
+            g.conv_in_c = c.in_c;
+            g.conv_kw = c.kw;
+            g.conv_wp = wp;
+            st = launch(s, "conv_gemm", [&] { return vh::launch_gemm(s.stream, g); });
+        }
+        if (!st)
+            st = launch(s, "conv_to_chw", [&] {
+                return vh::launch_padded_to_chw(s.stream, tmp, out, c.out_c, oh, ow, wp);
+            });
+        for (float *p : {xh, tmp})
+            if (p) hipFreeAsync(p, s.stream);
+        return st;
+    }
     if (c.hwc && !plain) {
         // Channel-last copy of the input, then one contiguous run per tap.
         st = dalloc(s, ih * iw * c.in_c, &xh, "convolution staging allocation");
@@ -1956,7 +1992,7 @@ vh_status conv_geometry(const vh_conv2d *c, const vh_tensor *input, size_t ih, s
     if (mul_overflows(npix, c->in_c * c->kh * c->kw, &cells) || cells > (size_t)INT32_MAX ||
         mul_overflows(npix, c->out_c, &outs) || outs > (size_t)INT32_MAX ||
         npix > (size_t)INT32_MAX / 2 || ih > INT32_MAX / 2 || iw > INT32_MAX / 2 ||
-        (npix + 31) / 32 > 65535)
+        (npix + 31) / 32 > 65535 || *oh > 65535)
         return fail(VH_ERR_KERNEL, "conv2d: shape exceeds the supported size");
     return VH_OK;
 }
