@@ -44,6 +44,9 @@ CONV_CASES = [
     (768, 768, 24, 36, 3, 2, 1),     # DPT resize layer 4 (3x3, stride 2)
     (64, 32, 48, 72, 3, 1, 1),       # head convolution
     (3, 4, 10, 11, 5, 3, 2),
+    (32, 16, 9, 11, 5, 1, 2),        # implicit GEMM, 5x5 taps, 4 junk columns per row
+    (64, 8, 7, 7, 3, 1, 0),          # implicit GEMM without padding
+    (96, 40, 13, 5, 1, 1, 1),        # implicit GEMM, 1x1 with padding
 ]
 
 
@@ -70,9 +73,10 @@ def test_conv2d_hand_checked_and_one_shot(rt):
     assert_bits_equal(a, rt.download_f32(c.run(rt.upload_f32(xs), 9, 9)), "one-shot vs prepared")
 
 
-def test_conv2d_relu_input_equals_materialised_relu(rt):
+@pytest.mark.parametrize("in_c", [32, 12])  # implicit GEMM / channel-last patch copy
+def test_conv2d_relu_input_equals_materialised_relu(rt, in_c):
     """src/conv.rs:1479-1520, on the device."""
-    in_c, out_c, h, w_ = 32, 24, 18, 27
+    out_c, h, w_ = 24, 18, 27
     x, w, b = _data(11, in_c * h * w_, out_c * in_c * 9, out_c)
     conv = rt.prepare_conv2d_f32(in_c, out_c, 3, 3, 1, 1, w, b)
     fused = rt.download_f32(conv.run_relu_input(rt.upload_f32(x), h, w_))
