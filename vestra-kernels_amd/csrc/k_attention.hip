@@ -643,13 +643,8 @@ template <bool TOKEN_MAJOR, int KVS, bool SPLIT>
 hipError_t run_flash(hipStream_t s, const FlashArgs &fa) {
     constexpr size_t lds = 2 * (size_t)KVS * (BKV * LDP + D * BKV) * sizeof(float);
     auto kernel = flash_kernel<TOKEN_MAJOR, KVS, SPLIT>;
-    static bool configured = false;
-    if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        configured = true;
-    }
+    static std::atomic<uint64_t> configured{0};
+    if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
     const int total = fa.bh * fa.qtiles * (SPLIT ? fa.splits : 1);
     const int grid = fa.xcd_map ? (total + 7) / 8 * 8 : total;
     kernel<<<grid, 256 * KVS, lds, s>>>(fa);
@@ -668,13 +663,8 @@ template <bool TOKEN_MAJOR, bool SPLIT>
 hipError_t run_flash_pipe(hipStream_t s, const FlashArgs &fa) {
     constexpr size_t lds = 2 * (size_t)(BKV * LDP + D * BKV) * sizeof(float);
     auto kernel = flash_pipe_kernel<TOKEN_MAJOR, SPLIT>;
-    static bool configured = false;
-    if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        configured = true;
-    }
+    static std::atomic<uint64_t> configured{0};
+    if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
     const int total = fa.bh * fa.qtiles * (SPLIT ? fa.splits : 1);
     const int grid = fa.xcd_map ? (total + 7) / 8 * 8 : total;
     kernel<<<grid, 256, lds, s>>>(fa);
