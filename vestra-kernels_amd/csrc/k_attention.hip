@@ -40,6 +40,10 @@ struct FlashArgs {
     int splits, split_keys;
     float *po;    // [splits][bh][T][64] unnormalised outputs
     float2 *pml;  // [splits][bh][T] (running max in the base-2 domain, sum)
+    // Token-major split runs only: when q8_qs is set, the merge writes the
+    // output rows as block-major Q8_0 (quantize_row_q8_0) instead of f32.
+    int8_t *q8_qs;
+    uint16_t *q8_d;
 };
 
 // V panels are stored transposed, Vt[d][key], so that the four keys a lane
@@ -628,15 +632,45 @@ __global__ __launch_bounds__(256) void flash_merge_kernel(FlashArgs fa) {
         acc += w * po[z];
     }
     const float inv = 1.0f / lsum;
+    const f32x4 o = acc * inv;
     float *dst;
     if constexpr (TOKEN_MAJOR) {
         const int bh = (int)(row / fa.T), query = (int)(row % fa.T);
         const int img = bh / fa.heads, head = bh % fa.heads;
+        if (fa.q8_qs) {
+            // Row img*T + query of the token-major [images*T][heads*64]
+            // output; a 32-column block is eight adjacent threads (d4 / 4 of
+            // one half of a head row), whose max takes three DPP steps.
+            float amax = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
+            amax = fmaxf(amax, dpp_f32<0xb1>(amax));
+            amax = fmaxf(amax, dpp_f32<0x4e>(amax));
+            amax = fmaxf(amax, dpp_f32<0x141>(amax));
+            const float d = div_rn(amax, 127.0f);
+            const float qinv = d != 0.0f ? div_rn(1.0f, d) : 0.0f;
+            uint32_t w = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float qv = roundf(mul_rn(o[e], qinv));  // f32::round: half away from zero
+                int qi;
+                if (isnan(qv)) {
+                    qi = 0;  // `NaN as i8` saturates to 0
+                } else {
+                    qv = fminf(fmaxf(qv, -127.0f), 127.0f);
+                    qi = (int)qv;
+                }
+                w |= ((uint32_t)(qi & 0xff)) << (8 * e);
+            }
+            const size_t M = (size_t)(fa.bh / fa.heads) * fa.T;
+            const size_t slot = (size_t)(head * 2 + (d4 >> 5)) * M + (size_t)img * fa.T + query;
+            reinterpret_cast<uint32_t *>(fa.q8_qs + slot * 32)[(d4 & 31) >> 2] = w;
+            if ((d4 & 31) == 0) fa.q8_d[slot] = __builtin_bit_cast(uint16_t, (_Float16)d);
+            return;
+        }
         dst = fa.out + ((size_t)img * fa.T + query) * ((size_t)fa.heads * D) + (size_t)head * D;
     } else {
         dst = fa.out + row * D;
     }
-    *reinterpret_cast<f32x4 *>(dst + d4) = acc * inv;
+    *reinterpret_cast<f32x4 *>(dst + d4) = o;
 }
 
 template <bool TOKEN_MAJOR, int KVS, bool SPLIT>
@@ -726,7 +760,9 @@ size_t flash_workspace_floats(size_t bh, size_t tokens) {
 
 hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k, const float *v,
                                   float *out, size_t bh, size_t tokens, size_t heads,
-                                  bool token_major, float *ws, size_t ws_floats) {
+                                  bool token_major, float *ws, size_t ws_floats, int8_t *q8_qs,
+                                  uint16_t *q8_d, bool *quantized) {
+    if (quantized) *quantized = false;
     if (bh == 0 || tokens == 0) return hipSuccess;
     FlashArgs fa{};
     fa.q = q;
@@ -787,6 +823,11 @@ hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k,
         fa.split_keys = split_keys(splits);
         fa.po = ws;
         fa.pml = reinterpret_cast<float2 *>(ws + (size_t)splits * bh * tokens * D);
+        if (token_major && q8_qs && q8_d) {
+            fa.q8_qs = q8_qs;
+            fa.q8_d = q8_d;
+            if (quantized) *quantized = true;
+        }
         if (pipe) return token_major ? run_flash_pipe<true, true>(s, fa) : run_flash_pipe<false, true>(s, fa);
         return token_major ? run_flash<true, 1, true>(s, fa) : run_flash<false, 1, true>(s, fa);
     }

@@ -72,6 +72,65 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
     reinterpret_cast<uint2 *>(qs + dst * 32)[part] = make_uint2(w[0], w[1]);
 }
 
+// LayerNorm of a row (the arithmetic of layernorm_kernel: ln_row_stats and
+// ln_apply) straight into Q8_0 blocks, bit-identical to LayerNorm followed by
+// quantize_q8_0_kernel.  One wave per row, float4 slot j of lane l holding
+// columns 4(l + 64j) .. +3, so a 32-column block is eight adjacent lanes and
+// its max takes three DPP steps (lane ^ 1, lane ^ 2, then the mirror that
+// pairs the two quads of eight lanes).  cols % 32 == 0, cols <= 1024.
+__global__ __launch_bounds__(256) void layernorm_q8_0_kernel(const float *__restrict__ in,
+                                                             const float *__restrict__ gamma,
+                                                             const float *__restrict__ beta,
+                                                             int8_t *__restrict__ qs,
+                                                             uint16_t *__restrict__ dbits,
+                                                             int rows, int cols, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const f32x4 *x = reinterpret_cast<const f32x4 *>(in + (size_t)row * cols);
+    const int n4 = cols >> 2;
+    f32x4 r[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int idx = lane + j * 64;
+        r[j] = idx < n4 ? x[idx] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    float mean, inv;
+    ln_row_stats(r, lane, n4, cols, eps, mean, inv);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int idx = lane + j * 64;
+        const bool live = idx < n4;  // whole 8-lane groups, as n4 % 8 == 0
+        const int gi = min(idx, n4 - 1);
+        const f32x4 y = ln_apply(r[j], mean, inv, reinterpret_cast<const f32x4 *>(gamma)[gi],
+                                 reinterpret_cast<const f32x4 *>(beta)[gi]);
+        float amax = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
+        amax = fmaxf(amax, dpp_f32<0xb1>(amax));
+        amax = fmaxf(amax, dpp_f32<0x4e>(amax));
+        amax = fmaxf(amax, dpp_f32<0x141>(amax));
+        const float d = div_rn(amax, 127.0f);
+        const float qinv = d != 0.0f ? div_rn(1.0f, d) : 0.0f;
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float q = roundf(mul_rn(y[e], qinv));  // f32::round: half away from zero
+            int qi;
+            if (isnan(q)) {
+                qi = 0;  // `NaN as i8` saturates to 0
+            } else {
+                q = fminf(fmaxf(q, -127.0f), 127.0f);
+                qi = (int)q;
+            }
+            w |= ((uint32_t)(qi & 0xff)) << (8 * e);
+        }
+        if (live) {
+            const size_t slot = (size_t)(idx >> 3) * rows + row;
+            reinterpret_cast<uint32_t *>(qs + slot * 32)[idx & 7] = w;
+            if ((idx & 7) == 0) dbits[slot] = __builtin_bit_cast(uint16_t, (_Float16)d);
+        }
+    }
+}
+
 // 256 threads = 4 waves in a 2x2 arrangement; each wave owns FM x FN MFMA
 // fragments of 16x16, so a workgroup covers (32*FM) x (32*FN) outputs (FM,
 // FN in {1, 2}: the small tiles give the narrow projections enough
@@ -98,6 +157,11 @@ struct Q8Epi {
     float *q, *k, *v;
     const float *rot;
     int tokens, heads;
+    // Gelu with FN == 2 and N % 32 == 0: when q8_qs is set, the GELU output
+    // is written as block-major Q8_0 rows (quantize_row_q8_0 of the f32
+    // values) instead of f32; c is unused.
+    int8_t *q8_qs;
+    uint16_t *q8_d;
 };
 
 template <Epi EPI, int FM, int FN>
@@ -257,6 +321,51 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
                     resid[i][j][r] = c[(size_t)min(mw + i * 16 + 4 * lh + r, M - 1) * N +
                                        min(nw + j * 16 + li, N - 1)];
     }
+    if constexpr (EPI == Epi::Gelu && FN == 2) {
+        if (ep.q8_qs) {
+            // A row's 32-column block nw .. nw + 31 is fragments j = 0, 1 of
+            // the 16 lanes sharing lh: its max takes four DPP steps within
+            // the 16-lane row.  Rows past M compute and are not stored.
+            const size_t kslice = (size_t)(nw >> 5);
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = mw + i * 16 + 4 * lh + r;
+                    float g[2];
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        const size_t idx = (size_t)row * N + nw + j * 16 + li;
+                        float v = acc[i][j][r];
+                        if (ep.bias) v = add_rn(v, bias[j]);
+                        g[j] = idx < ep.tail_start ? gelu_avx512_form(v) : gelu_scalar_form(v);
+                    }
+                    float amax = fmaxf(fabsf(g[0]), fabsf(g[1]));
+                    amax = fmaxf(amax, dpp_f32<0xb1>(amax));
+                    amax = fmaxf(amax, dpp_f32<0x4e>(amax));
+                    amax = fmaxf(amax, dpp_f32<0x141>(amax));
+                    amax = fmaxf(amax, dpp_f32<0x140>(amax));
+                    const float d = div_rn(amax, 127.0f);
+                    const float qinv = d != 0.0f ? div_rn(1.0f, d) : 0.0f;
+                    if (row >= M) continue;
+                    const size_t slot = kslice * M + row;
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        float q = roundf(mul_rn(g[j], qinv));  // f32::round: half away from zero
+                        int qi;
+                        if (isnan(q)) {
+                            qi = 0;  // `NaN as i8` saturates to 0
+                        } else {
+                            q = fminf(fmaxf(q, -127.0f), 127.0f);
+                            qi = (int)q;
+                        }
+                        ep.q8_qs[slot * 32 + j * 16 + li] = (int8_t)qi;
+                    }
+                    if (li == 0) ep.q8_d[slot] = __builtin_bit_cast(uint16_t, (_Float16)d);
+                }
+            return;
+        }
+    }
     if constexpr (EPI == Epi::Qkv) {
         // The wave's 32 columns are one axis half of one head (N is a
         // multiple of 64): fragment j = 0 holds dims d0 + li, j = 1 holds
@@ -378,15 +487,39 @@ static bool q8_operands_fit(size_t m, size_t n, size_t k) {
     return m * k <= (size_t)INT32_MAX && n * k <= (size_t)INT32_MAX;
 }
 
+hipError_t launch_layernorm_q8_0(hipStream_t s, const float *x, const float *gamma,
+                                 const float *beta, int8_t *qs, uint16_t *d, size_t rows,
+                                 size_t cols, float eps) {
+    if (rows == 0) return hipSuccess;
+    if (cols % 32 != 0 || cols > 1024 || cols == 0 || rows > (size_t)INT32_MAX / 4 ||
+        ((((uintptr_t)x) | ((uintptr_t)gamma) | ((uintptr_t)beta)) & 15) != 0)
+        return hipErrorInvalidValue;
+    layernorm_q8_0_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(x, gamma, beta, qs, d,
+                                                                     (int)rows, (int)cols, eps);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm_q8_0(hipStream_t s, const int8_t *a_qs, const uint16_t *a_d,
                             const int8_t *b_qs, const uint16_t *b_d, float *c, size_t m,
-                            size_t n, size_t k, Epi epi, const float *bias, const float *gamma) {
+                            size_t n, size_t k, Epi epi, const float *bias, const float *gamma,
+                            int8_t *q8_qs, uint16_t *q8_d, bool *quantized) {
+    if (quantized) *quantized = false;
     if (m == 0 || n == 0) return hipSuccess;
     if (!q8_operands_fit(m, n, k)) return hipErrorInvalidValue;
     Q8Epi ep{};
     ep.bias = bias;
     ep.gamma = gamma;
     ep.tail_start = m * n - (m * n) % 16;
+    if (epi == Epi::Gelu && q8_qs && q8_d && n % 32 == 0) {
+        int fm, fn;
+        q8_tile(m, n, &fm, &fn);
+        if (fn == 2) {
+            // The quantised GELU output needs whole 32-column blocks per wave.
+            ep.q8_qs = q8_qs;
+            ep.q8_d = q8_d;
+            if (quantized) *quantized = true;
+        }
+    }
     switch (epi) {
         case Epi::Store: q8_dispatch<Epi::Store>(s, a_qs, a_d, b_qs, b_d, c, m, n, k, ep); break;
         case Epi::Gelu: q8_dispatch<Epi::Gelu>(s, a_qs, a_d, b_qs, b_d, c, m, n, k, ep); break;

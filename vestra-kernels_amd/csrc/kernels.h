@@ -55,9 +55,15 @@ hipError_t launch_attention_online(hipStream_t s, const float *q, const float *k
 // floats; with ws == nullptr (or too small) the kernel runs unsplit.
 constexpr int kMaxFlashSplits = 4;
 size_t flash_workspace_floats(size_t bh, size_t tokens);
+// With q8_qs / q8_d (token-major only) a run that splits the keys writes its
+// output as block-major Q8_0 rows [images*tokens][heads*64] from the merge
+// (bit-identical to the f32 output quantised) and sets *quantized; otherwise
+// the f32 output is written and *quantized is false.
 hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k, const float *v,
                                   float *out, size_t bh, size_t tokens, size_t heads,
-                                  bool token_major, float *ws, size_t ws_floats);
+                                  bool token_major, float *ws, size_t ws_floats,
+                                  int8_t *q8_qs = nullptr, uint16_t *q8_d = nullptr,
+                                  bool *quantized = nullptr);
 
 // ---- DPT head (k_dpt.hip) ------------------------------------------------
 // colT [oh*ow][in_c*kh*kw] of a CHW input (zero padding; ReLU on the input
@@ -132,12 +138,21 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs &g);
 // x [rows][k] -> block-major Q8_0: qs [k/32][rows][32] int8, d [k/32][rows] f16 bits
 hipError_t launch_quantize_q8_0(hipStream_t s, const float *x, int8_t *qs, uint16_t *d,
                                 size_t rows, size_t k);
+// LayerNorm of each row straight into block-major Q8_0 (bit-identical to
+// launch_layernorm then launch_quantize_q8_0); cols % 32 == 0, cols <= 1024.
+hipError_t launch_layernorm_q8_0(hipStream_t s, const float *x, const float *gamma,
+                                 const float *beta, int8_t *qs, uint16_t *d, size_t rows,
+                                 size_t cols, float eps);
 // c = a . b^T block by block (exact int sums, block-order f32 fold), then the
 // epilogue (Store / Gelu / Residual, see k_q8.hip); bias / gamma may be null.
 hipError_t launch_gemm_q8_0(hipStream_t s, const int8_t *a_qs, const uint16_t *a_d,
                             const int8_t *b_qs, const uint16_t *b_d, float *c, size_t m,
                             size_t n, size_t k, Epi epi = Epi::Store, const float *bias = nullptr,
-                            const float *gamma = nullptr);
+                            const float *gamma = nullptr, int8_t *q8_qs = nullptr,
+                            uint16_t *q8_d = nullptr, bool *quantized = nullptr);
+// (Gelu with q8_qs / q8_d: when the tile allows, the GELU output is written
+// as block-major Q8_0 rows, bit-identical to the f32 output quantised, and
+// *quantized is set; otherwise c receives f32 and *quantized is false.)
 // The QKV projection in Q8_0 (n = 3*heads*64): bias, then q/k/v head-major
 // [img][head][token][64] with the 2-D RoPE of q and k when rot is non-null
 // (rot [tokens][2][16][sin, cos]); m must be a multiple of tokens.

@@ -367,7 +367,8 @@ vh_status splitk_workspace(RtState &s, size_t m, size_t n, float **out, size_t *
 }
 
 vh_status flash(RtState &s, const float *q, const float *k, const float *v, float *out,
-                size_t bh, size_t tokens, size_t heads, bool token_major) {
+                size_t bh, size_t tokens, size_t heads, bool token_major, int8_t *q8_qs = nullptr,
+                uint16_t *q8_d = nullptr, bool *quantized = nullptr) {
     // Partials of the key splits; without them the kernel runs unsplit.
     const size_t need = vh::flash_workspace_floats(bh, tokens);
     if (s.fw_floats < need) {
@@ -380,7 +381,7 @@ vh_status flash(RtState &s, const float *q, const float *k, const float *v, floa
     }
     return launch(s, "flash_attention", [&] {
         return vh::launch_flash_attention(s.stream, q, k, v, out, bh, tokens, heads, token_major,
-                                          s.fw, s.fw_floats);
+                                          s.fw, s.fw_floats, q8_qs, q8_d, quantized);
     });
 }
 
@@ -474,32 +475,46 @@ vh_status q8_workspace(RtState &s, size_t rows, size_t k, int8_t **qs, uint16_t 
     return VH_OK;
 }
 
-// The engine's Q8_0 projection: quantise the input rows (quantize_row_q8_0),
-// block-dot GEMM against the weight blocks, then the epilogue.
-vh_status run_q8(RtState &s, const Q8Lin &L, const float *in, size_t rows, vh::Epi epi, float *c,
-                 const char *name) {
+// Q8_0 activation rows in the runtime workspace: quantize_row_q8_0 of `in`,
+// or, with norm, the LayerNorm of `in` quantised in the same kernel.
+struct Q8Rows {
     int8_t *qs = nullptr;
     uint16_t *d = nullptr;
-    TRY(q8_workspace(s, rows, L.K, &qs, &d));
-    TRY(launch(s, "quantize_q8_0", [&] {
-        return vh::launch_quantize_q8_0(s.stream, in, qs, d, rows, L.K);
-    }));
+};
+vh_status q8_rows(RtState &s, const float *in, size_t rows, size_t k, const RowNorm *norm,
+                  Q8Rows *out) {
+    TRY(q8_workspace(s, rows, k, &out->qs, &out->d));
+    if (norm)
+        return launch(s, "layernorm_q8_0", [&] {
+            return vh::launch_layernorm_q8_0(s.stream, in, norm->gamma, norm->beta, out->qs,
+                                             out->d, rows, k, norm->eps);
+        });
+    return launch(s, "quantize_q8_0", [&] {
+        return vh::launch_quantize_q8_0(s.stream, in, out->qs, out->d, rows, k);
+    });
+}
+
+// The engine's Q8_0 projection: quantise the input rows (quantize_row_q8_0;
+// with norm, of LayerNorm(in)), block-dot GEMM against the weight blocks,
+// then the epilogue.
+vh_status run_q8(RtState &s, const Q8Lin &L, const float *in, size_t rows, vh::Epi epi, float *c,
+                 const char *name, const RowNorm *norm = nullptr) {
+    Q8Rows a;
+    TRY(q8_rows(s, in, rows, L.K, norm, &a));
     return launch(s, name, [&] {
-        return vh::launch_gemm_q8_0(s.stream, qs, d, L.qs, L.d, c, rows, L.N, L.K, epi, L.bias,
+        return vh::launch_gemm_q8_0(s.stream, a.qs, a.d, L.qs, L.d, c, rows, L.N, L.K, epi, L.bias,
                                     epi == vh::Epi::Gelu ? nullptr : L.gamma);
     });
 }
 
 // The QKV projection in Q8_0, written head-major with the RoPE when rot is set.
 vh_status run_q8_qkv(RtState &s, const Q8Lin &L, const float *in, size_t images, size_t tokens,
-                     const float *rot, float *q, float *k, float *v) {
+                     const float *rot, float *q, float *k, float *v, const RowNorm *norm = nullptr) {
     const size_t rows = images * tokens;
-    int8_t *qs = nullptr;
-    uint16_t *d = nullptr;
-    TRY(q8_workspace(s, rows, L.K, &qs, &d));
-    TRY(launch(s, "quantize_q8_0", [&] {
-        return vh::launch_quantize_q8_0(s.stream, in, qs, d, rows, L.K);
-    }));
+    Q8Rows a;
+    TRY(q8_rows(s, in, rows, L.K, norm, &a));
+    int8_t *qs = a.qs;
+    uint16_t *d = a.d;
     return launch(s, "gemm_q8_0_qkv", [&] {
         return vh::launch_gemm_q8_0_qkv(s.stream, qs, d, L.qs, L.d, rows, L.K, L.bias, q, k, v,
                                         tokens, L.N / 192, rot);
@@ -1684,31 +1699,61 @@ vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size
         std::vector<int64_t> zero(tokens * 2, 0);
         TRY(rope_table(s, zero.data(), tokens, 64, freq, &rot));
     }
-    if (!h_ready)
-        TRY(launch(s, "layernorm", [&] {
-            return vh::launch_layernorm(s.stream, x, b.ln1_g, b.ln1_b, h, M, D, eps);
-        }));
     if (b.q8) {
-        // Q8_0 projections: each GEMM quantises its input rows first, so no
-        // LayerNorm rides in a GEMM epilogue and fc2 leaves the next block's
-        // LayerNorm1 to that block.
+        // Q8_0 projections: each GEMM takes Q8_0 rows, so the LayerNorms
+        // write Q8_0 directly (h_ready: the previous f32 block left
+        // LayerNorm1(x) in h, which is quantised), and fc2 leaves the next
+        // block's LayerNorm1 to that block.
+        const RowNorm ln1{b.ln1_g, b.ln1_b, nullptr, eps};
+        const float *qin = h_ready ? h : x;
+        const RowNorm *n1 = h_ready ? nullptr : &ln1;
         if (b.qn_g) {
-            TRY(run_q8_qkv(s, b.qqkv, h, images, tokens, nullptr, q, k, v));
+            TRY(run_q8_qkv(s, b.qqkv, qin, images, tokens, nullptr, q, k, v, n1));
             TRY(launch(s, "qk_norm_rope", [&] {
                 return vh::launch_qk_norm_rope(s.stream, q, k, b.qn_g, b.qn_b, b.kn_g, b.kn_b,
                                                rot, M * kHeads, tokens, eps);
             }));
         } else {
-            TRY(run_q8_qkv(s, b.qqkv, h, images, tokens, rot, q, k, v));
+            TRY(run_q8_qkv(s, b.qqkv, qin, images, tokens, rot, q, k, v, n1));
         }
-        TRY(flash(s, q, k, v, att, images * kHeads, tokens, kHeads, true));
-        TRY(run_q8(s, b.qproj, att, M, vh::Epi::Residual, x, "gemm_q8_0_proj_residual"));
-        TRY(launch(s, "layernorm", [&] {
-            return vh::launch_layernorm(s.stream, x, b.ln2_g, b.ln2_b, h, M, D, eps);
+        // The attention merge writes Q8_0 rows directly when the keys are
+        // split; otherwise the f32 output is quantised.
+        Q8Rows a;
+        TRY(q8_workspace(s, M, D, &a.qs, &a.d));
+        bool quantized = false;
+        TRY(flash(s, q, k, v, att, images * kHeads, tokens, kHeads, true, a.qs, a.d, &quantized));
+        if (!quantized)
+            TRY(launch(s, "quantize_q8_0", [&] {
+                return vh::launch_quantize_q8_0(s.stream, att, a.qs, a.d, M, D);
+            }));
+        TRY(launch(s, "gemm_q8_0_proj_residual", [&] {
+            return vh::launch_gemm_q8_0(s.stream, a.qs, a.d, b.qproj.qs, b.qproj.d, x, M, D, D,
+                                        vh::Epi::Residual, b.qproj.bias, b.qproj.gamma);
         }));
-        TRY(run_q8(s, b.qfc1, h, M, vh::Epi::Gelu, f, "gemm_q8_0_fc1_gelu"));
-        return run_q8(s, b.qfc2, f, M, vh::Epi::Residual, x, "gemm_q8_0_fc2_residual");
+        // fc1 quantises its GELU output for fc2 in its epilogue when its
+        // tile allows (the f32 output is quantised otherwise).  Its input
+        // rows and its output rows need separate Q8_0 buffers: the output
+        // goes to the block workspace, past the f32 rows of f.
+        const RowNorm ln2{b.ln2_g, b.ln2_b, nullptr, eps};
+        Q8Rows hin;
+        TRY(q8_rows(s, x, M, D, &ln2, &hin));
+        int8_t *fq = reinterpret_cast<int8_t *>(f);  // M x kMlp bytes of values ...
+        uint16_t *fd = reinterpret_cast<uint16_t *>(fq + M * kMlp);  // ... then the scales
+        bool fq_ready = false;
+        TRY(launch(s, "gemm_q8_0_fc1_gelu", [&] {
+            return vh::launch_gemm_q8_0(s.stream, hin.qs, hin.d, b.qfc1.qs, b.qfc1.d, f, M, kMlp,
+                                        D, vh::Epi::Gelu, b.qfc1.bias, nullptr, fq, fd, &fq_ready);
+        }));
+        if (!fq_ready) return run_q8(s, b.qfc2, f, M, vh::Epi::Residual, x, "gemm_q8_0_fc2_residual");
+        return launch(s, "gemm_q8_0_fc2_residual", [&] {
+            return vh::launch_gemm_q8_0(s.stream, fq, fd, b.qfc2.qs, b.qfc2.d, x, M, D, kMlp,
+                                        vh::Epi::Residual, b.qfc2.bias, b.qfc2.gamma);
+        });
     }
+    if (!h_ready)
+        TRY(launch(s, "layernorm", [&] {
+            return vh::launch_layernorm(s.stream, x, b.ln1_g, b.ln1_b, h, M, D, eps);
+        }));
     if (b.qn_g) {
         // Late block: QKV with bias only, then LayerNorm of every 64-wide Q
         // and K head row fused with the RoPE (src/specialized.rs:278-316).
