@@ -157,3 +157,20 @@ def test_late_block_needs_all_four_qk_norm_vectors(rt):
     del w["k_norm_beta"]
     with pytest.raises(vh.InvalidArgument):
         rt.prepare_block(w)
+
+
+def test_empty_inputs_are_no_ops(rt):
+    """Zero tokens or images: the block, the encoder and the Q8_0 block return
+    without launching; zero layers leave x unchanged."""
+    w = da3.block_weights(seed=27)
+    blk, qblk = rt.prepare_block(w), rt.prepare_block(w, q8_0=True)
+    empty = rt.upload_f32(np.zeros(0, np.float32))
+    rt.vit_block_run(blk, empty, 1, 0)
+    rt.vit_block_run(qblk, empty, 0, 865)
+    rt.encoder_run([blk, qblk], empty, 2, 0)
+    x = seeded.normal(2700, 97 * 768)
+    xt = rt.upload_f32(x)
+    rt.encoder_run([], xt, 1, 97)
+    assert np.array_equal(rt.download_f32(xt), x)
+    with pytest.raises(vh.LengthMismatch):
+        rt.vit_block_run(blk, xt, 1, 98)
