@@ -90,10 +90,11 @@ def test_encoder_config5a_batch4_12_layers(rt):
     assert max_rel(got, exp) <= ENCODER_TOL
 
 
-def test_encoder_config5b_long_sequence_2_layers(rt):
-    """1008x672 -> 48 x 72 grid + CLS = 3457 tokens (non-flash CPU path).  Two
-    layers keep the CPU oracle's generic attention to seconds."""
-    got, exp, x = _encoder_case(rt, images=1, rows=48, cols=72, layers=2)
+def test_encoder_config5b_long_sequence_12_layers(rt):
+    """1008x672 -> 48 x 72 grid + CLS = 3457 tokens (the CPU oracle takes the
+    crate's generic attention path, not the 865-token flash gate), the full
+    12 layers of BASELINE config 5 (about 1 s of oracle time per layer)."""
+    got, exp, x = _encoder_case(rt, images=1, rows=48, cols=72, layers=12)
     assert max_rel(got, exp) <= ENCODER_TOL
 
 
