@@ -392,23 +392,27 @@ def test_gemm_q8_0_bit_exact(rt, m, n, k):
 
 
 def test_flash_key_layouts_deterministic_and_consistent(rt, monkeypatch):
-    """Every key layout -- one or two key streams per workgroup (merged in
-    stream order through LDS), or keys split over 2-4 workgroups (merged in
-    split order by a second kernel) -- gives run-to-run identical results, and
-    all agree to rounding.  1-, 64- and 65-token shapes leave the second
-    stream without valid keys; 130 tokens gives a split of one short panel."""
-    layouts = (("1", "1"), ("1", "2"), ("2", "1"), ("3", "1"), ("4", "1"))
+    """Every key layout -- one key stream per workgroup (direct-to-LDS panels,
+    or register-staged panels with DIRECT=0), two streams per workgroup
+    (merged in stream order through LDS), or keys split over 2-4 workgroups
+    (merged in split order by a second kernel) -- gives run-to-run identical
+    results, and all agree to rounding.  1-, 64- and 65-token shapes leave
+    the second stream without valid keys; 130 tokens gives a split of one
+    short panel."""
+    layouts = (("1", "1", "1"), ("1", "1", "0"), ("1", "2", "1"), ("2", "1", "1"),
+               ("3", "1", "1"), ("3", "1", "0"), ("4", "1", "1"))
     for H, T in ((12, 865), (2, 1), (2, 64), (2, 65), (1, 130)):
         n = H * T * 64
         q, k, v = (rt.upload_f32(seeded.normal(s + T, n)) for s in (31, 32, 33))
         outs = {}
-        for splits, streams in layouts:
+        for splits, streams, direct in layouts:
             monkeypatch.setenv("VESTRA_HIP_FLASH_SPLITS", splits)
             monkeypatch.setenv("VESTRA_HIP_FLASH_STREAMS", streams)
+            monkeypatch.setenv("VESTRA_HIP_FLASH_DIRECT", direct)
             a = rt.download_f32(rt.flash_attention_f32_da3_base(q, k, v, H, T))
             b = rt.download_f32(rt.flash_attention_f32_da3_base(q, k, v, H, T))
-            assert_bits_equal(a, b, f"flash splits={splits} streams={streams} rerun")
+            assert_bits_equal(a, b, f"flash splits={splits} streams={streams} direct={direct} rerun")
             assert np.isfinite(a).all()
-            outs[(splits, streams)] = a
+            outs[(splits, streams, direct)] = a
         for key, a in outs.items():
-            assert max_rel(a, outs[("1", "1")]) <= 2e-6, (H, T, key)
+            assert max_rel(a, outs[("1", "1", "1")]) <= 2e-6, (H, T, key)

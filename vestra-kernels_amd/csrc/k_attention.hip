@@ -15,6 +15,12 @@
 // the sum is reduced once at the end.  Exponentials run in base 2 with the
 // 1/8 * log2(e) scale folded into one multiply.
 //
+// flash_direct_kernel: the same work split for one key stream per
+// workgroup, with K/V panels copied straight from global memory into LDS
+// and V kept row-major (P is the A operand of the second contraction); it
+// is the default for one-stream layouts, flash_kernel serves two-stream
+// layouts.
+//
 // attention_online_kernel: the reference device kernel's contract
 // (src/cuda.rs:153-194): any head_dim <= 64, one thread per (head, query).
 #include <cstdlib>
@@ -316,23 +322,46 @@ __global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2)
         *reinterpret_cast<f32x4 *>(orow + 16 * df + 4 * lh) = o[df] * inv;
 }
 
-// Software-pipelined form for one key stream per workgroup: while the
-// MFMAs of S(j+1) = K(j+1) . Q^T run, the same wave's VALU computes the
-// online softmax of panel j, so MFMA and softmax no longer alternate.  LDS
-// stage j holds K(j+1) and V(j) (keys lead values by one panel): iteration j
-// reads stage j and fills stage j+1 with K(j+2), V(j+1), in the buffer that
-// last held stage j-1, read before the previous barrier.  The last panel is
-// peeled so no MFMA work goes to a panel that does not exist.  Two
-// workgroups share a CU (two waves per SIMD), so a wave has 256 registers.
+// Direct-to-LDS form for one key stream per workgroup (two workgroups per
+// CU).  Panels of K and V go from global memory straight into LDS with
+// global_load_lds_dwordx4 (no register staging, no LDS stores): instruction
+// i of wave w copies keys 4c..4c+3 (c = 4i + w), lane L writing the 16-byte
+// granule L%16 of key 4c + L/16.  The wave picks which global granule each
+// lane fetches, so K is XOR-swizzled on the way in (global granule g of key
+// r lands at granule g ^ (r & 15)) and a 16-lane group reading one granule
+// column of 16 keys hits 16 distinct bank groups.
+//
+// V stays row-major, because the second contraction takes P as the A
+// operand and V as B:
+//     O[query][d] += P[query][key] . V[key][d]   (d = 4*li + df for output
+//                                                 fragment df of lane li)
+// The score registers of S^T = K.Q^T already hold P[query li][keys
+// 16g+4lh+r], i.e. the A operand of k-step (g, r); lane (li, lh) feeds B
+// with V[16g+4lh+r][4li+df] for df = 0..3 -- one 16-byte read per k-step
+// serving four MFMAs.  The output fragment of lane (li, lh) then holds
+// queries 4lh+r, whose softmax corrections live in lanes 4lh+r: four lane
+// shuffles per panel carry them over.
+//
+// Per panel: one barrier (after which the panel's copies, issued one panel
+// earlier, have landed and every wave is done with the buffer being
+// refilled), the 16 K fragment reads, the copies of the next panel, then
+// the QK MFMAs with one V fragment read after every four, the softmax, and
+// the PV MFMAs.
+using lds_ptr = __attribute__((address_space(3))) void *;
+using global_ptr = __attribute__((address_space(1))) void *;
+constexpr int PANEL = BKV * D;  // floats of one K or V panel (16 KB)
+
+// Each lane copies the 16 bytes at src to lds_wave + 16 * lane.
+__device__ __forceinline__ void copy_to_lds16(const float *src, float *lds_wave) {
+    __builtin_amdgcn_global_load_lds((global_ptr)src, (lds_ptr)lds_wave, 16, 0, 0);
+}
+
 template <bool TOKEN_MAJOR, bool SPLIT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_pipe_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_direct_kernel(
     FlashArgs fa) {
-    constexpr int NT = 256;
-    constexpr int KSTAGE = BKV * LDP;  // floats of one K stage
-    constexpr int VSTAGE = D * BKV;    // floats of one V^T stage
     extern __shared__ __attribute__((aligned(16))) float smem[];
-    float *Ks = smem;               // [2][BKV*LDP]
-    float *Vs = smem + 2 * KSTAGE;  // [2][D*BKV], transposed and swizzled
+    float *Ks = smem;              // [2][64 keys][64], swizzled granules
+    float *Vs = smem + 2 * PANEL;  // [2][64 keys][64]
 
     const int splits = SPLIT ? fa.splits : 1;
     const int total = fa.bh * fa.qtiles * splits;
@@ -355,101 +384,94 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const float *Qh = fa.q + head_off;
     const float *Kh = fa.k + head_off;
     const float *Vh = fa.v + head_off;
-    const int query = qt * BQ + wave * 16 + li;
+    const int qw = qt * BQ + wave * 16;  // this wave's first query
+    const int query = qw + li;
     f32x4 qf[4];
 #pragma unroll
     for (int c = 0; c < 4; c++)
         qf[c] = query < T ? *reinterpret_cast<const f32x4 *>(Qh + (size_t)query * D + 16 * c + 4 * lh)
                           : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    constexpr int CH = BKV * 16 / NT;  // float4 chunks per thread and panel (= 4)
-    f32x4 rk[CH], rv[CH];
-    auto gload_k = [&](int k0) {
+    // Keys past ke copy key ke - 1: finite values whose scores are masked.
+    auto copy_panel = [&](int buf, int k0) {
 #pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
-            rk[i] = *reinterpret_cast<const f32x4 *>(Kh + (size_t)min(k0 + key, ke - 1) * D + d4);
+        for (int i = 0; i < 4; i++) {
+            const int c = 4 * i + wave;
+            const int key = 4 * c + lh;
+            const size_t row = (size_t)min(k0 + key, ke - 1) * D;
+            copy_to_lds16(Kh + row + 4 * (li ^ (key & 15)), Ks + buf * PANEL + c * 256);
+            copy_to_lds16(Vh + row + 4 * li, Vs + buf * PANEL + c * 256);
         }
     };
-    auto gload_v = [&](int k0) {
+
+    const float scale = 0.125f * kLog2e;
+    float m = -INFINITY;  // running max (base 2) of query li
+    float l = 0.0f;       // partial running sum over this lane's keys
+    f32x4 o[4];           // o[df][r] = O[query qw + 4lh + r][4li + df] (unnormalised)
 #pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
-            rv[i] = *reinterpret_cast<const f32x4 *>(Vh + (size_t)min(k0 + key, ke - 1) * D + d4);
-        }
-    };
-    auto store_k = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
-            *reinterpret_cast<f32x4 *>(&Ks[buf * KSTAGE + key * LDP + d4]) = rk[i];
-        }
-    };
-    auto store_v = [&](int buf, int k0) {
-#pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const int c = tid + i * NT, key = c >> 4, d4 = (c & 15) * 4;
-            const unsigned keep = k0 + key < ke ? 0xffffffffu : 0u;  // keys past ke: +0 rows
-            float *vt = Vs + buf * VSTAGE;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int d = d4 + e;
-                vt[d * BKV + (key ^ vswz(d))] = __uint_as_float(__float_as_uint(rv[i][e]) & keep);
-            }
-        }
-    };
-    int vcol[4];
-#pragma unroll
-    for (int df = 0; df < 4; df++) vcol[df] = vswz(16 * df + li);
-    f32x4 kf[4][4], vf[4][4];
-    auto read_kf = [&](int buf) {
-        const float *ks = Ks + buf * KSTAGE + li * LDP + 4 * lh;
+    for (int i = 0; i < 4; i++) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int n = (ke - kb + BKV - 1) / BKV;  // panels, >= 1
+    copy_panel(0, kb);
+    for (int j = 0; j < n; j++) {
+        const int buf = j & 1;
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of panel j
+        __syncthreads();
+        const float *ks = Ks + buf * PANEL;
+        const float *vs = Vs + buf * PANEL + (4 * lh) * D + 4 * li;
+        f32x4 kf[4][4], vf[4][4];  // kf[g][c] = K[16g + li][16c + 4lh ..]
 #pragma unroll
         for (int c = 0; c < 4; c++)
 #pragma unroll
             for (int g = 0; g < 4; g++)
-                kf[g][c] = *reinterpret_cast<const f32x4 *>(&ks[16 * g * LDP + 16 * c]);
-    };
-    auto read_vf = [&](int buf) {
-        const float *vt = Vs + buf * VSTAGE;
+                kf[g][c] = *reinterpret_cast<const f32x4 *>(&ks[(16 * g + li) * D + 4 * ((4 * c + lh) ^ li)]);
+        if (j + 1 < n) copy_panel(buf ^ 1, kb + (j + 1) * BKV);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int g = 0; g < 4; g++)
 #pragma unroll
-            for (int df = 0; df < 4; df++)
-                vf[g][df] = *reinterpret_cast<const f32x4 *>(
-                    &vt[(16 * df + li) * BKV + ((16 * g + 4 * lh) ^ vcol[df])]);
-    };
-    // S^T fragments: s[g][r] = S[key 16g+4lh+r][query li].
-    auto qk = [&](f32x4 (&sc)[4]) {
+            for (int st = 0; st < 4; st++)
+                vf[g][st] = *reinterpret_cast<const f32x4 *>(&vs[(16 * g + st) * D]);
+        // S^T fragments: s[g][r] = S[key 16g+4lh+r][query li].
+        f32x4 s[4];
 #pragma unroll
-        for (int g = 0; g < 4; g++) sc[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int g = 0; g < 4; g++) s[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int c = 0; c < 4; c++)
 #pragma unroll
             for (int st = 0; st < 4; st++)
 #pragma unroll
-                for (int g = 0; g < 4; g++) sc[g] = mfma16x16x4(kf[g][c][st], qf[c][st], sc[g]);
-    };
-    const float scale = 0.125f * kLog2e;
-    float m = -INFINITY, l = 0.0f;
-    f32x4 o[4];
+                for (int g = 0; g < 4; g++) s[g] = mfma16x16x4(kf[g][c][st], qf[c][st], s[g]);
 #pragma unroll
-    for (int i = 0; i < 4; i++) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // Online softmax of panel k0 in place (scores -> probabilities).
-    auto softmax = [&](f32x4 (&sc)[4], int k0) {
+        for (int i = 0; i < 16; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // Online softmax of query li over its 16 keys of the panel.  The max
+        // is taken on the raw scores (the scale is positive) and the scale
+        // is folded into the exponent's FMA; full panels need no mask.
+        const int k0 = kb + j * BKV;
         float mx = -INFINITY;
+        if (k0 + BKV <= ke) {
 #pragma unroll
-        for (int g = 0; g < 4; g++)
+            for (int g = 0; g < 4; g++)
+                mx = fmaxf(mx, fmaxf(fmaxf(s[g][0], s[g][1]), fmaxf(s[g][2], s[g][3])));
+        } else {
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int key = k0 + 16 * g + 4 * lh + r;
-                const float t = key < ke ? sc[g][r] * scale : -INFINITY;
-                sc[g][r] = t;
-                mx = fmaxf(mx, t);
-            }
+            for (int g = 0; g < 4; g++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int key = k0 + 16 * g + 4 * lh + r;
+                    s[g][r] = key < ke ? s[g][r] : -INFINITY;
+                    mx = fmaxf(mx, s[g][r]);
+                }
+        }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mnew = fmaxf(m, mx);
+        const float mnew = fmaxf(m, mx * scale);
+        // A range with no valid key yet keeps m = -inf; 0 as the reference
+        // makes exp2 see -inf (giving 0), never NaN.
         const float mref = mnew == -INFINITY ? 0.0f : mnew;
         const float corr = __builtin_amdgcn_exp2f(m - mref);
         float psum = 0.0f;
@@ -457,150 +479,58 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int g = 0; g < 4; g++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float pv = __builtin_amdgcn_exp2f(sc[g][r] - mref);
-                sc[g][r] = pv;
-                psum += pv;
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][r], scale, -mref));
+                s[g][r] = p;
+                psum += p;
             }
         l = l * corr + psum;
         m = mnew;
 #pragma unroll
-        for (int df = 0; df < 4; df++) o[df] *= corr;
-    };
-    // O^T[d][query] += V^T[d][key] P^T[key][query].
-    auto pv = [&](const f32x4 (&pr)[4]) {
+        for (int r = 0; r < 4; r++) {
+            const float cr = __shfl(corr, 4 * lh + r, 64);
+#pragma unroll
+            for (int df = 0; df < 4; df++) o[df][r] *= cr;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // O[q][4li + df] += P[q][key] V[key][4li + df], key = 16g + 4lh + st.
 #pragma unroll
         for (int g = 0; g < 4; g++)
 #pragma unroll
             for (int st = 0; st < 4; st++)
 #pragma unroll
-                for (int df = 0; df < 4; df++) o[df] = mfma16x16x4(vf[g][df][st], pr[g][st], o[df]);
-    };
-
-    const int n = (ke - kb + BKV - 1) / BKV;  // panels of this workgroup, >= 1
-    auto pk = [&](int j) { return kb + min(j, n - 1) * BKV; };
-
-    // Prologue: K(0) into buffer 1, S(0); stage 0 = K(1), V(0) into buffer 0.
-    gload_k(pk(0));
-    store_k(1);
-    gload_k(pk(1));
-    gload_v(pk(0));
-    __syncthreads();
-    f32x4 s_cur[4], s_next[4];
-    read_kf(1);
-    qk(s_cur);
-    store_k(0);
-    store_v(0, pk(0));
-    __syncthreads();
-
-    for (int j = 0; j + 1 < n; j++) {
-        const int buf = j & 1;
-        // QK phase: K(j+2) and V(j+1) are fetched, K(j+1) is read, and the QK
-        // MFMAs of panel j+1 run with the softmax VALU work of panel j
-        // between them.
-        gload_k(pk(j + 2));
-        gload_v(pk(j + 1));
-        read_kf(buf);
-        __builtin_amdgcn_sched_barrier(0);
-        // The 64 QK MFMAs go out in 16 steps of four (one (c, st) k-slice for
-        // the four key groups); after each step comes one sixteenth of the
-        // softmax of panel j, fenced so that the compiler keeps the order.
-        {
-            const int k0 = kb + j * BKV;
-            float mxg[4], mx = 0.0f, sh = 0.0f, mnew = 0.0f, mref = 0.0f, corr = 0.0f, psum = 0.0f;
-#pragma unroll
-            for (int g = 0; g < 4; g++) s_next[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int step = 0; step < 16; step++) {
-                const int c = step >> 2, st = step & 3;
-#pragma unroll
-                for (int g = 0; g < 4; g++) s_next[g] = mfma16x16x4(kf[g][c][st], qf[c][st], s_next[g]);
-                if (step < 4) {  // scale and mask key group g = step
-                    const int g = step;
-                    float mg = -INFINITY;
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int key = k0 + 16 * g + 4 * lh + r;
-                        const float t = key < ke ? s_cur[g][r] * scale : -INFINITY;
-                        s_cur[g][r] = t;
-                        mg = fmaxf(mg, t);
-                    }
-                    mxg[g] = mg;
-                } else if (step == 4) {  // each shuffle is used one step after its issue
-                    mx = fmaxf(fmaxf(mxg[0], mxg[1]), fmaxf(mxg[2], mxg[3]));
-                    sh = __shfl_xor(mx, 16, 64);
-                } else if (step == 5) {
-                    mx = fmaxf(mx, sh);
-                    sh = __shfl_xor(mx, 32, 64);
-                } else if (step == 6) {
-                    mx = fmaxf(mx, sh);
-                    mnew = fmaxf(m, mx);
-                    // A key range with no valid key yet keeps m = -inf; 0 as
-                    // the reference makes exp2 see -inf (giving 0), never NaN.
-                    mref = mnew == -INFINITY ? 0.0f : mnew;
-                    corr = __builtin_amdgcn_exp2f(m - mref);
-                } else if (step < 11) {  // probabilities of key group g
-                    const int g = step - 7;
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const float pv = __builtin_amdgcn_exp2f(s_cur[g][r] - mref);
-                        s_cur[g][r] = pv;
-                        psum += pv;
-                    }
-                } else if (step == 11) {
-                    l = l * corr + psum;
-                    m = mnew;
-                } else {  // rescale output fragment df
-                    o[step - 12] *= corr;
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        // Stage j+1 (K(j+2), V(j+1)) goes into the other buffer, which last
-        // held stage j-1, read before the previous barrier; the loads have
-        // had the whole QK phase to arrive.
-        store_k(buf ^ 1);
-        store_v(buf ^ 1, pk(j + 1));
-        __builtin_amdgcn_sched_barrier(0);
-        // PV phase: the V fragments of key group g+1 are read during the
-        // MFMAs of group g, so only one fragment set is live at a time.
-        read_vf(buf);
-        pv(s_cur);
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-        for (int i = 0; i < 12; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-        __syncthreads();
-#pragma unroll
-        for (int g = 0; g < 4; g++) s_cur[g] = s_next[g];
+                for (int df = 0; df < 4; df++) o[df] = mfma16x16x4(s[g][st], vf[g][st][df], o[df]);
     }
-    read_vf((n - 1) & 1);
-    softmax(s_cur, kb + (n - 1) * BKV);
-    pv(s_cur);
 
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    if (query >= T) return;
-    if constexpr (SPLIT) {
-        const size_t prow = ((size_t)z * fa.bh + bh) * T + query;
-        float *orow = fa.po + prow * D;
+    // Output row r of this lane is query qw + 4lh + r, whose (m, l) sit in
+    // lane 4lh + r.
+    float lr[4], mr[4];
 #pragma unroll
-        for (int df = 0; df < 4; df++) *reinterpret_cast<f32x4 *>(orow + 16 * df + 4 * lh) = o[df];
-        if (lh == 0) fa.pml[prow] = make_float2(m, l);
-        return;
-    }
-    const float inv = 1.0f / l;
-    float *orow;
-    if constexpr (TOKEN_MAJOR) {
-        const int img = bh / fa.heads, head = bh % fa.heads;
-        orow = fa.out + ((size_t)img * T + query) * ((size_t)fa.heads * D) + (size_t)head * D;
-    } else {
-        orow = fa.out + head_off + (size_t)query * D;
+    for (int r = 0; r < 4; r++) {
+        lr[r] = __shfl(l, 4 * lh + r, 64);
+        mr[r] = __shfl(m, 4 * lh + r, 64);
     }
 #pragma unroll
-    for (int df = 0; df < 4; df++) *reinterpret_cast<f32x4 *>(orow + 16 * df + 4 * lh) = o[df] * inv;
+    for (int r = 0; r < 4; r++) {
+        const int qr = qw + 4 * lh + r;
+        if (qr >= T) continue;
+        const f32x4 v = f32x4{o[0][r], o[1][r], o[2][r], o[3][r]};
+        if constexpr (SPLIT) {
+            const size_t prow = ((size_t)z * fa.bh + bh) * T + qr;
+            *reinterpret_cast<f32x4 *>(fa.po + prow * D + 4 * li) = v;
+            if (li == 0) fa.pml[prow] = make_float2(mr[r], lr[r]);
+        } else {
+            float *orow;
+            if constexpr (TOKEN_MAJOR) {
+                const int img = bh / fa.heads, head = bh % fa.heads;
+                orow = fa.out + ((size_t)img * T + qr) * ((size_t)fa.heads * D) + (size_t)head * D;
+            } else {
+                orow = fa.out + head_off + (size_t)qr * D;
+            }
+            *reinterpret_cast<f32x4 *>(orow + 4 * li) = v * (1.0f / lr[r]);
+        }
+    }
 }
 
 // Combines the key splits of each (head, query) in split order:
@@ -694,9 +624,9 @@ hipError_t run_flash(hipStream_t s, const FlashArgs &fa) {
 }
 
 template <bool TOKEN_MAJOR, bool SPLIT>
-hipError_t run_flash_pipe(hipStream_t s, const FlashArgs &fa) {
-    constexpr size_t lds = 2 * (size_t)(BKV * LDP + D * BKV) * sizeof(float);
-    auto kernel = flash_pipe_kernel<TOKEN_MAJOR, SPLIT>;
+hipError_t run_flash_direct(hipStream_t s, const FlashArgs &fa) {
+    constexpr size_t lds = 2 * (size_t)(2 * PANEL) * sizeof(float);
+    auto kernel = flash_direct_kernel<TOKEN_MAJOR, SPLIT>;
     static std::atomic<uint64_t> configured{0};
     if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
     const int total = fa.bh * fa.qtiles * (SPLIT ? fa.splits : 1);
@@ -814,10 +744,10 @@ hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k,
     if (const char *e = std::getenv("VESTRA_HIP_FLASH_STREAMS"))
         if (splits == 1) streams = std::atoi(e) == 2 ? 2 : 1;
 
-    // One-stream layouts run the software-pipelined kernel
-    // (VESTRA_HIP_FLASH_PIPE=0 selects the plain loop for A/B runs).
-    bool pipe = true;
-    if (const char *e = std::getenv("VESTRA_HIP_FLASH_PIPE")) pipe = std::atoi(e) != 0;
+    // One-stream layouts run the direct-to-LDS kernel
+    // (VESTRA_HIP_FLASH_DIRECT=0 selects the register-staged loop for A/B runs).
+    bool direct = true;
+    if (const char *e = std::getenv("VESTRA_HIP_FLASH_DIRECT")) direct = std::atoi(e) != 0;
     if (splits > 1) {
         fa.splits = splits;
         fa.split_keys = split_keys(splits);
@@ -828,14 +758,16 @@ hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k,
             fa.q8_d = q8_d;
             if (quantized) *quantized = true;
         }
-        if (pipe) return token_major ? run_flash_pipe<true, true>(s, fa) : run_flash_pipe<false, true>(s, fa);
+        if (direct)
+            return token_major ? run_flash_direct<true, true>(s, fa) : run_flash_direct<false, true>(s, fa);
         return token_major ? run_flash<true, 1, true>(s, fa) : run_flash<false, 1, true>(s, fa);
     }
     fa.splits = 1;
     fa.split_keys = (int)tokens;
     if (streams == 2)
         return token_major ? run_flash<true, 2, false>(s, fa) : run_flash<false, 2, false>(s, fa);
-    if (pipe) return token_major ? run_flash_pipe<true, false>(s, fa) : run_flash_pipe<false, false>(s, fa);
+    if (direct)
+        return token_major ? run_flash_direct<true, false>(s, fa) : run_flash_direct<false, false>(s, fa);
     return token_major ? run_flash<true, 1, false>(s, fa) : run_flash<false, 1, false>(s, fa);
 }
 
