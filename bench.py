@@ -308,8 +308,9 @@ def gpu_dpt(reps: int = 20) -> dict:
                                      "conv_to_chw") if k in prof}
     conv_us = sum(conv_parts.values())
     t_flops = 2.0 * th * tw * tc * tc * 16
-    t_parts = {"to_hwc": us("conv_transpose_to_hwc"), "gemm": us("conv_transpose_gemm"),
-               "scatter": us("patch_scatter")}
+    t_parts = {label: us(k) for label, k in (("to_hwc", "conv_transpose_to_hwc"),
+                                             ("gemm", "conv_transpose_gemm"),
+                                             ("scatter", "patch_scatter")) if k in prof}
     t_us = sum(t_parts.values())
     r_us = us("bilinear_align_corners")
     r_bytes = 4.0 * c * (rh * rw + 4 * rh * rw)

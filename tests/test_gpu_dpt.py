@@ -99,8 +99,14 @@ def test_conv2d_resize_add_equals_materialised_route(rt):
     assert_bits_equal(fused, mat, "fused resize route")
 
 
-@pytest.mark.parametrize("in_c, out_c, ih, iw, k", [(96, 96, 24, 36, 4), (192, 192, 24, 36, 2),
-                                                    (3, 4, 3, 2, 2), (16, 8, 3, 5, 4)])
+@pytest.mark.parametrize("in_c, out_c, ih, iw, k", [
+    (96, 96, 24, 36, 4),    # DA3 k4s4: patch-scatter GEMM, 16-byte stores
+    (192, 192, 24, 36, 2),  # k2s2: patch-scatter GEMM, element stores
+    (32, 5, 7, 9, 4),       # 80 weight rows: a partial row tile, 63 pixels
+    (64, 3, 5, 6, 2),       # 12 weight rows
+    (32, 7, 4, 5, 3),       # k3s3: rows do not align to (oc, ky) groups of 4
+    (3, 4, 3, 2, 2),        # in_c % 32 != 0: GEMM into a staging buffer, then the scatter
+    (16, 8, 3, 5, 4)])
 def test_conv_transpose_nonoverlap_vs_naive(rt, in_c, out_c, ih, iw, k):
     x, w, b = _data(0xFEED1234 + in_c, in_c * ih * iw, in_c * out_c * k * k, out_c)
     ct = rt.prepare_conv_transpose2d_f32(in_c, out_c, k, k, k, w, b)

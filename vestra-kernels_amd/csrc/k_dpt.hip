@@ -125,27 +125,6 @@ __global__ __launch_bounds__(256) void chw_to_padded_hwc_kernel(const float *__r
     }
 }
 
-// [oh * wp][oc] on the padded grid -> CHW [oc][oh][ow], dropping the wp - ow
-// junk columns of each row.  grid.z is the output row.
-__global__ __launch_bounds__(256) void padded_to_chw_kernel(const float *__restrict__ cp,
-                                                            float *__restrict__ out, int oc,
-                                                            int oh, int ow, int wp) {
-    __shared__ float tile[32][33];
-    const int x0 = blockIdx.x * 32, c0 = blockIdx.y * 32, oy = blockIdx.z;
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int x = x0 + ty + 8 * k, ch = c0 + tx;
-        tile[ty + 8 * k][tx] = (x < ow && ch < oc) ? cp[((size_t)oy * wp + x) * oc + ch] : 0.0f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int ch = c0 + ty + 8 * k, x = x0 + tx;
-        if (ch < oc && x < ow) out[((size_t)ch * oh + oy) * ow + x] = tile[tx][ty + 8 * k];
-    }
-}
-
 // out[oc][iy*kh+ky][ix*kw+kx] = c[iy*iw+ix][(oc*kh+ky)*kw+kx]: one thread per
 // output element, so the writes are coalesced.
 __global__ __launch_bounds__(256) void patch_scatter_kernel(const float *__restrict__ c,
@@ -303,15 +282,6 @@ hipError_t launch_chw_to_padded_hwc(hipStream_t s, const float *in, float *xp, s
     if (grid.y > 65535) return hipErrorInvalidValue;
     chw_to_padded_hwc_kernel<<<grid, 256, 0, s>>>(in, xp, (int)c, (int)ih, (int)iw, (int)pad,
                                                   (int)(iw + 2 * pad), (int)rows, relu ? 1 : 0);
-    return hipGetLastError();
-}
-
-hipError_t launch_padded_to_chw(hipStream_t s, const float *cp, float *out, size_t oc, size_t oh,
-                                size_t ow, size_t wp) {
-    if (oc == 0 || oh == 0 || ow == 0) return hipSuccess;
-    const dim3 grid((unsigned)((ow + 31) / 32), (unsigned)((oc + 31) / 32), (unsigned)oh);
-    if (grid.y > 65535 || grid.z > 65535) return hipErrorInvalidValue;
-    padded_to_chw_kernel<<<grid, 256, 0, s>>>(cp, out, (int)oc, (int)oh, (int)ow, (int)wp);
     return hipGetLastError();
 }
 

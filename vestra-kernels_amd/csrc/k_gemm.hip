@@ -37,10 +37,17 @@ struct EpiArgs {
     const float *rot;
     size_t tail_start;
     float *partial;  // split-K: raw partial tiles [split][M][N]
-    // Implicit convolution (CONV kernels): A is a zero-padded channel-last
-    // image [rows][conv_in_c] and row m of the GEMM's A for k-slice k0 is
-    // image row m + (ky * conv_wp + kx), tap = k0 / conv_in_c = ky * conv_kw + kx.
-    int conv_in_c, conv_kw, conv_wp;
+    // Implicit convolution (CONV kernels): Bt is a zero-padded channel-last
+    // image [rows][conv_in_c] and row n of the GEMM's Bt for k-slice k0 is
+    // image row n + (ky * conv_wp + kx), tap = k0 / conv_in_c = ky * conv_kw + kx.
+    // C[m][n] (out channel m, padded-grid position n = y * conv_wp + x) goes
+    // to c[m * conv_plane + y * conv_ow + x] for x < conv_ow.
+    int conv_in_c, conv_kw, conv_wp, conv_ow;
+    size_t conv_plane;
+    // Patch scatter (CONV == 2, a kernel == stride transposed convolution):
+    // C[m = (oc * kh + ky) * kw + kx][n = iy * iw + ix] goes to
+    // c[oc][iy * kh + ky][ix * kw + kx]; bias is per row m.
+    int scat_kh, scat_kw, scat_iw;
 };
 
 // Applies a Store / Gelu / Residual epilogue to one output element.
@@ -97,10 +104,14 @@ __device__ __forceinline__ void tile_of_block(bool xcd_order, int &tm, int &tn, 
 // or columns past the edge are never stored.  Selecting on the loaded value
 // would make the compiler wait for the prefetch before the MFMAs of the
 // current slice, so the load path stays select-free.
-// CONV (EXACT only): the A rows of a k-slice are the padded image rows of
+// CONV (EXACT only): the Bt rows of a k-slice are the padded image rows of
 // one convolution tap, shifted by that tap's offset (see EpiArgs); conv_in_c
-// is a multiple of BK, so a slice never straddles two taps.
-template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, bool CONV = false>
+// is a multiple of BK, so a slice never straddles two taps.  A is the weight
+// [out_c][K], so the output tile is channel-major and is written straight to
+// the CHW output.  CONV == 2 (EXACT only) is a plain GEMM whose tile rows
+// are (out channel, tap) and columns input pixels, stored by the patch
+// scatter of EpiArgs.
+template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, int CONV = 0>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__restrict__ A,
                                                               const float *__restrict__ Bt,
                                                               int M, int N, int K,
@@ -135,24 +146,25 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
 
     f32x4 ra[ACH], rb[BCH];
     auto gload = [&](int k0) {
-        if constexpr (EXACT && CONV) {
-            const int tap = k0 / ep.conv_in_c;
-            const int shift = (tap / ep.conv_kw) * ep.conv_wp + tap % ep.conv_kw;
-            const int kin = k0 - tap * ep.conv_in_c;
-#pragma unroll
-            for (int i = 0; i < ACH; i++) {
-                int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
-                ra[i] = *reinterpret_cast<const f32x4 *>(
-                    A + ((size_t)min(m0 + row, M - 1) + shift) * ep.conv_in_c + kin + kq);
-            }
-        } else if constexpr (EXACT) {
+        if constexpr (EXACT) {
 #pragma unroll
             for (int i = 0; i < ACH; i++) {
                 int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
                 ra[i] = *reinterpret_cast<const f32x4 *>(A + (size_t)min(m0 + row, M - 1) * K + k0 + kq);
             }
         }
-        if constexpr (EXACT) {
+        if constexpr (EXACT && CONV == 1) {
+            const int tap = k0 / ep.conv_in_c;
+            const int shift = (tap / ep.conv_kw) * ep.conv_wp + tap % ep.conv_kw;
+            const int kin = k0 - tap * ep.conv_in_c;
+#pragma unroll
+            for (int i = 0; i < BCH; i++) {
+                int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
+                rb[i] = *reinterpret_cast<const f32x4 *>(
+                    Bt + ((size_t)min(n0 + row, N - 1) + shift) * ep.conv_in_c + kin + kq);
+            }
+            return;
+        } else if constexpr (EXACT) {
 #pragma unroll
             for (int i = 0; i < BCH; i++) {
                 int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
@@ -303,6 +315,74 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                 for (int r = 0; r < 4; r++) {
                     const int row = rbase + i * 16 + r;
                     if (row < M) part[(size_t)row * N + col] = acc[i][j][r];
+                }
+        }
+    } else if constexpr (CONV == 2) {
+        // Row m = (oc, ky, kx), column n = input pixel (iy, ix): the output
+        // element (oc, iy * kh + ky, ix * kw + kx).  A lane's four rows 4lh..
+        // 4lh+3 are kx = 0..3 of one (oc, ky) when kw == 4 (rows are aligned to
+        // 4), i.e. one 16-byte store, and the 16 lanes of a group store 16
+        // consecutive pixels of one output row.
+        const int kh = ep.scat_kh, kw = ep.scat_kw, iw = ep.scat_iw;
+        const int ow = iw * kw;
+        const size_t plane = (size_t)(N / iw) * kh * ow;
+        const int cbase = n0 + wn * TN + li;
+        float bias[FM][4];
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) bias[i][r] = ep.bias ? ep.bias[min(rbase + i * 16 + r, M - 1)] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int n = cbase + j * 16;
+            if (n >= N) continue;
+            const int iy = n / iw, ix = n - iy * iw;
+#pragma unroll
+            for (int i = 0; i < FM; i++) {
+                const int m4 = rbase + i * 16;  // multiple of 4
+                f32x4 v;
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[r] = ep.bias ? add_rn(acc[i][j][r], bias[i][r]) : acc[i][j][r];
+                if (kw == 4 && m4 + 3 < M) {
+                    const int oc = m4 / (4 * kh), ky = (m4 / 4) % kh;
+                    *reinterpret_cast<f32x4 *>(ep.c + oc * plane + (size_t)(iy * kh + ky) * ow + ix * 4) = v;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int m = m4 + r;
+                        if (m >= M) continue;
+                        const int kx = m % kw, ky = (m / kw) % kh, oc = m / (kw * kh);
+                        ep.c[oc * plane + (size_t)(iy * kh + ky) * ow + ix * kw + kx] = v[r];
+                    }
+                }
+            }
+        }
+    } else if constexpr (CONV == 1) {
+        // Output channel m = row, padded-grid position n = column: conv + bias
+        // to CHW, dropping the wp - ow junk columns.  The 16 lanes of a lane
+        // group store 16 consecutive positions of one channel.
+        float bias[FM][4];
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) bias[i][r] = ep.bias ? ep.bias[min(rbase + i * 16 + r, M - 1)] : 0.0f;
+        const int cbase = n0 + wn * TN + li;
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int n = cbase + j * 16;
+            if (n >= N) continue;
+            const int y = n / ep.conv_wp, x = n - y * ep.conv_wp;
+            if (x >= ep.conv_ow) continue;
+            const size_t pix = (size_t)y * ep.conv_ow + x;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = rbase + i * 16 + r;
+                    if (row >= M) continue;
+                    float v = acc[i][j][r];
+                    if (ep.bias) v = add_rn(v, bias[i][r]);
+                    ep.c[(size_t)row * ep.conv_plane + pix] = v;
                 }
         }
     } else if constexpr (EPI == Epi::Qkv) {
@@ -543,7 +623,7 @@ struct Tile {
     int bm, bn, bk, wm, wn;
 };
 
-template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, bool CONV = false>
+template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, int CONV = 0>
 hipError_t launch_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int splits, int kps) {
     constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 4) * sizeof(float);
     auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, SPLIT, EXACT, CONV>;
@@ -676,13 +756,20 @@ hipError_t dispatch_conv(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
     const int kps = (int)g.k;
 #define VH_CONV_TILE(BM, BN, BK, WM, WN)                                                    \
     if (t.bm == BM && t.bn == BN && t.bk == BK && t.wm == WM && t.wn == WN)                 \
-        return launch_tile<BM, BN, BK, WM, WN, Epi::Store, false, true, true>(s, g, ep, 1, kps);
+        return launch_tile<BM, BN, BK, WM, WN, Epi::Store, false, true, 1>(s, g, ep, 1, kps);
     VH_CONV_TILE(64, 64, 32, 2, 2)
     VH_CONV_TILE(128, 128, 32, 2, 4)
     VH_CONV_TILE(64, 128, 64, 2, 4)
     VH_CONV_TILE(64, 128, 32, 2, 4)
 #undef VH_CONV_TILE
-    return launch_tile<64, 64, 32, 2, 2, Epi::Store, false, true, true>(s, g, ep, 1, kps);
+    return launch_tile<64, 64, 32, 2, 2, Epi::Store, false, true, 1>(s, g, ep, 1, kps);
+}
+
+// Patch-scatter GEMM (k % 32 == 0): one 64 x 64 x 32 tile shape, since the
+// row count (out_c * kh * kw) and the pixel count are both moderate.
+hipError_t dispatch_scatter(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
+    if (g.k % 32 != 0 || g.k == 0) return hipErrorInvalidValue;
+    return launch_tile<64, 64, 32, 2, 2, Epi::Store, false, true, 2>(s, g, ep, 1, (int)g.k);
 }
 
 }  // namespace
@@ -740,10 +827,23 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs &g) {
     ep.tail_start = total - total % 16;
     if (g.conv_in_c) {
         if (g.epi != Epi::Store) return hipErrorInvalidValue;
+        if (g.conv_ow == 0 || g.conv_ow > g.conv_wp || g.n % g.conv_wp != 0)
+            return hipErrorInvalidValue;
         ep.conv_in_c = (int)g.conv_in_c;
         ep.conv_kw = (int)g.conv_kw;
         ep.conv_wp = (int)g.conv_wp;
+        ep.conv_ow = (int)g.conv_ow;
+        ep.conv_plane = g.n / g.conv_wp * g.conv_ow;
         return dispatch_conv(s, g, ep);
+    }
+    if (g.scatter_kw) {
+        if (g.epi != Epi::Store || g.scatter_kh == 0 || g.scatter_iw == 0 ||
+            g.m % (g.scatter_kh * g.scatter_kw) != 0 || g.n % g.scatter_iw != 0)
+            return hipErrorInvalidValue;
+        ep.scat_kh = (int)g.scatter_kh;
+        ep.scat_kw = (int)g.scatter_kw;
+        ep.scat_iw = (int)g.scatter_iw;
+        return dispatch_scatter(s, g, ep);
     }
     switch (g.epi) {
         case Epi::Store: return dispatch<Epi::Store>(s, g, ep);

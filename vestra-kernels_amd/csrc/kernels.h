@@ -80,9 +80,6 @@ hipError_t launch_im2col_hwc(hipStream_t s, const float *xh, float *col, size_t 
 // (iw + 2 pad) grid (rows past the grid are zeros; ReLU when relu).
 hipError_t launch_chw_to_padded_hwc(hipStream_t s, const float *in, float *xp, size_t c,
                                     size_t ih, size_t iw, size_t pad, size_t rows, bool relu);
-// [oh * wp][oc] on a padded grid -> CHW [oc][oh][ow] (drops wp - ow columns).
-hipError_t launch_padded_to_chw(hipStream_t s, const float *cp, float *out, size_t oc, size_t oh,
-                                size_t ow, size_t wp);
 // c [ih*iw][out_c*kh*kw] -> out [out_c][ih*kh][iw*kw] (kernel == stride).
 hipError_t launch_patch_scatter(hipStream_t s, const float *c, float *out, size_t out_c,
                                 size_t ih, size_t iw, size_t kh, size_t kw);
@@ -123,14 +120,22 @@ struct GemmArgs {
     const float *ln_gamma = nullptr, *ln_beta = nullptr;
     float *ln_out = nullptr;
     float ln_eps = 0.0f;
-    // Implicit stride-1 convolution (Store only): a is a zero-padded
-    // channel-last image [rows][conv_in_c] of row width conv_wp, m counts
-    // output positions on that padded grid, and bt is the weight
-    // [out_c][kh][kw][conv_in_c] (k = tap * conv_in_c + ic, tap = ky * conv_kw
-    // + kx); A row m of tap (ky, kx) is image row m + ky * conv_wp + kx, so
-    // the image needs (kh - 1) * conv_wp + conv_kw - 1 rows past m.
-    // conv_in_c must be a multiple of 32.
-    size_t conv_in_c = 0, conv_kw = 0, conv_wp = 0;
+    // Implicit stride-1 convolution (Store only): a is the weight
+    // [out_c][kh][kw][conv_in_c] (m = out_c, k = tap * conv_in_c + ic, tap =
+    // ky * conv_kw + kx), bt is a zero-padded channel-last image
+    // [rows][conv_in_c] of row width conv_wp, and n counts output positions
+    // on that padded grid (n = oh * conv_wp); Bt row n of tap (ky, kx) is
+    // image row n + ky * conv_wp + kx, so the image needs (kh - 1) * conv_wp
+    // + conv_kw - 1 rows past n.  c receives the CHW output [m][oh][conv_ow]
+    // (bias per output channel; the conv_wp - conv_ow junk columns are not
+    // stored).  conv_in_c must be a multiple of 32.
+    size_t conv_in_c = 0, conv_kw = 0, conv_wp = 0, conv_ow = 0;
+    // Patch scatter of a kernel == stride transposed convolution (Store
+    // only, k % 32 == 0): a is the weight [out_c * kh * kw][k], bt the
+    // channel-last input [ih * iw][k] (n = ih * iw), and C[(oc * kh + ky) * kw
+    // + kx][iy * iw + ix] + bias[row] goes to the CHW output
+    // c[oc][iy * kh + ky][ix * kw + kx].
+    size_t scatter_kh = 0, scatter_kw = 0, scatter_iw = 0;
 };
 hipError_t launch_gemm(hipStream_t s, const GemmArgs &g);
 

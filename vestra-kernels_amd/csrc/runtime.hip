@@ -1959,12 +1959,12 @@ vh_status conv_run(RtState &s, const vh_conv2d &c, const float *in, size_t ih, s
     vh_status st = VH_OK;
     if (c.hwc && c.stride == 1 && c.in_c % 32 == 0 && !plain) {
         // Implicit GEMM: the GEMM reads each tap's rows straight from the
-        // zero-padded channel-last image and computes the outputs on the
-        // padded grid (wp - ow junk columns per row, dropped at the end).
+        // zero-padded channel-last image, computes the outputs on the padded
+        // grid (wp - ow junk columns per row) with the output channels as
+        // rows, and stores the CHW output directly, junk columns dropped.
         const size_t wp = iw + 2 * c.pad, hp = ih + 2 * c.pad;
-        const size_t rows = hp * wp + c.kw - 1, m = oh * wp;
+        const size_t rows = hp * wp + c.kw - 1;
         st = dalloc(s, rows * c.in_c, &xh, "convolution staging allocation");
-        if (!st) st = dalloc(s, m * c.out_c, &tmp, "convolution output allocation");
         if (!st)
             st = launch(s, "conv_to_padded_hwc", [&] {
                 return vh::launch_chw_to_padded_hwc(s.stream, in, xh, c.in_c, ih, iw, c.pad, rows,
@@ -1972,25 +1972,21 @@ vh_status conv_run(RtState &s, const vh_conv2d &c, const float *in, size_t ih, s
             });
         if (!st) {
             vh::GemmArgs g{};
-            g.a = xh;
-            g.bt = c.w;
-            g.m = m;
-            g.n = c.out_c;
+            g.a = c.w;
+            g.bt = xh;
+            g.m = c.out_c;
+            g.n = oh * wp;
             g.k = K;
             g.epi = vh::Epi::Store;
-            g.c = tmp;
+            g.c = out;
             g.bias = c.bias;
             g.conv_in_c = c.in_c;
             g.conv_kw = c.kw;
             g.conv_wp = wp;
+            g.conv_ow = ow;
             st = launch(s, "conv_gemm", [&] { return vh::launch_gemm(s.stream, g); });
         }
-        if (!st)
-            st = launch(s, "conv_to_chw", [&] {
-                return vh::launch_padded_to_chw(s.stream, tmp, out, c.out_c, oh, ow, wp);
-            });
-        for (float *p : {xh, tmp})
-            if (p) hipFreeAsync(p, s.stream);
+        if (xh) hipFreeAsync(xh, s.stream);
         return st;
     }
     if (c.hwc && !plain) {
@@ -2181,7 +2177,33 @@ vh_status conv_t_new(const vh_conv_transpose2d *c, const vh_tensor *input, size_
     vh_tensor *t = nullptr;
     TRY(new_tensor(c->rt, olen, &t, "conv_transpose2d output allocation"));
     vh_status st = VH_OK;
-    if (c->nonoverlap) {
+    if (c->nonoverlap && c->in_c % 32 == 0) {
+        // Channel-last input, then one GEMM with the weight rows (oc, ky, kx)
+        // as the tile rows, stored straight to CHW by its patch-scatter
+        // epilogue.
+        float *xt = nullptr;
+        st = dalloc(s, plane * c->in_c, &xt, "conv_transpose2d staging allocation");
+        if (!st)
+            st = launch(s, "conv_transpose_to_hwc", [&] {
+                return vh::launch_transpose(s.stream, input->ptr, xt, c->in_c, plane);
+            });
+        if (!st) {
+            vh::GemmArgs g{};
+            g.a = c->w;
+            g.bt = xt;
+            g.m = c->out_c * c->kh * c->kw;
+            g.n = plane;
+            g.k = c->in_c;
+            g.epi = vh::Epi::Store;
+            g.c = t->ptr;
+            g.bias = c->bias_x;
+            g.scatter_kh = c->kh;
+            g.scatter_kw = c->kw;
+            g.scatter_iw = iw;
+            st = launch(s, "conv_transpose_gemm", [&] { return vh::launch_gemm(s.stream, g); });
+        }
+        if (xt) hipFreeAsync(xt, s.stream);
+    } else if (c->nonoverlap) {
         const size_t cols = c->out_c * c->kh * c->kw;
         float *xt = nullptr, *tmp = nullptr;
         st = dalloc(s, plane * c->in_c, &xt, "conv_transpose2d staging allocation");
