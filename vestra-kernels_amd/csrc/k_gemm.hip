@@ -48,6 +48,10 @@ struct EpiArgs {
     // C[m = (oc * kh + ky) * kw + kx][n = iy * iw + ix] goes to
     // c[oc][iy * kh + ky][ix * kw + kx]; bias is per row m.
     int scat_kh, scat_kw, scat_iw;
+    // Direct convolution (CONV == 3): Bt is the CHW image [conv_in_c][cd_ih]
+    // [cd_iw] read in place; column n is output pixel (n / conv_ow, n %
+    // conv_ow) and the output is c[m * N + n]; ReLU on the image when cd_relu.
+    int cd_ih, cd_iw, cd_stride, cd_pad, cd_relu;
 };
 
 // Applies a Store / Gelu / Residual epilogue to one output element.
@@ -110,7 +114,12 @@ __device__ __forceinline__ void tile_of_block(bool xcd_order, int &tm, int &tn, 
 // [out_c][K], so the output tile is channel-major and is written straight to
 // the CHW output.  CONV == 2 (EXACT only) is a plain GEMM whose tile rows
 // are (out channel, tap) and columns input pixels, stored by the patch
-// scatter of EpiArgs.
+// scatter of EpiArgs.  CONV == 3 (EXACT only) reads the Bt tile straight
+// from a CHW image: a thread owns one output pixel of the tile and 8
+// channels of the k-slice, so 64 lanes load 64 consecutive pixels of one
+// channel; taps outside the image load a clamped in-range pixel and are
+// zeroed when the slice is stored to LDS (after the MFMAs), and the output
+// is the channel-major tile itself, i.e. CHW.
 template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, int CONV = 0>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__restrict__ A,
                                                               const float *__restrict__ Bt,
@@ -144,6 +153,24 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     const int kend = min(K, kbeg + k_per_split);
     const bool vec = (K & 3) == 0;
 
+    // CONV == 3: this thread's pixel (tile column cd_p), channel group and
+    // the image position of its (0, 0) tap; cd_ok marks whether the tap of
+    // the prefetched slice lies inside the image.
+    int cd_p = 0, cd_cg = 0, cd_y = 0, cd_x = 0;
+    bool cd_live = false, cd_ok = false;
+    if constexpr (CONV == 3) {
+        static_assert(BN * BK == 8 * NT && NT % BN == 0 && BCH == 2,
+                      "direct convolution: one pixel x 8 channels per thread");
+        cd_p = tid % BN;
+        cd_cg = tid / BN;
+        const int n = n0 + cd_p;
+        cd_live = n < N;
+        const int nc = min(n, N - 1);
+        const int y = nc / ep.conv_ow, x = nc - y * ep.conv_ow;
+        cd_y = y * ep.cd_stride - ep.cd_pad;
+        cd_x = x * ep.cd_stride - ep.cd_pad;
+    }
+
     f32x4 ra[ACH], rb[BCH];
     auto gload = [&](int k0) {
         if constexpr (EXACT) {
@@ -162,6 +189,20 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                 int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
                 rb[i] = *reinterpret_cast<const f32x4 *>(
                     Bt + ((size_t)min(n0 + row, N - 1) + shift) * ep.conv_in_c + kin + kq);
+            }
+            return;
+        } else if constexpr (EXACT && CONV == 3) {
+            const int tap = k0 / ep.conv_in_c, kin = k0 - tap * ep.conv_in_c;
+            const int ky = tap / ep.conv_kw, kx = tap - ky * ep.conv_kw;
+            const int yi = cd_y + ky, xi = cd_x + kx;
+            cd_ok = cd_live && yi >= 0 && yi < ep.cd_ih && xi >= 0 && xi < ep.cd_iw;
+            const size_t hw = (size_t)ep.cd_ih * ep.cd_iw;
+            const float *src = Bt + (size_t)(kin + 8 * cd_cg) * hw +
+                               (size_t)min(max(yi, 0), ep.cd_ih - 1) * ep.cd_iw + min(max(xi, 0), ep.cd_iw - 1);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                rb[0][e] = src[e * hw];
+                rb[1][e] = src[(e + 4) * hw];
             }
             return;
         } else if constexpr (EXACT) {
@@ -209,10 +250,25 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
             int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
             *reinterpret_cast<f32x4 *>(&as[row * LDK + kq]) = ra[i];
         }
+        if constexpr (CONV == 3) {
+            // Pixel cd_p, channels 8 cd_cg .. +7 of the slice: ReLU on the
+            // image values when asked, zeros for taps outside the image.
 #pragma unroll
-        for (int i = 0; i < BCH; i++) {
-            int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
-            *reinterpret_cast<f32x4 *>(&bs[row * LDK + kq]) = rb[i];
+            for (int i = 0; i < 2; i++) {
+                f32x4 v = rb[i];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    if (ep.cd_relu) v[e] = fmaxf(v[e], 0.0f);
+                    v[e] = cd_ok ? v[e] : 0.0f;
+                }
+                *reinterpret_cast<f32x4 *>(&bs[cd_p * LDK + 8 * cd_cg + 4 * i]) = v;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < BCH; i++) {
+                int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
+                *reinterpret_cast<f32x4 *>(&bs[row * LDK + kq]) = rb[i];
+            }
         }
     };
 
@@ -357,7 +413,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                 }
             }
         }
-    } else if constexpr (CONV == 1) {
+    } else if constexpr (CONV == 1 || CONV == 3) {
         // Output channel m = row, padded-grid position n = column: conv + bias
         // to CHW, dropping the wp - ow junk columns.  The 16 lanes of a lane
         // group store 16 consecutive positions of one channel.
@@ -371,9 +427,12 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
         for (int j = 0; j < FN; j++) {
             const int n = cbase + j * 16;
             if (n >= N) continue;
-            const int y = n / ep.conv_wp, x = n - y * ep.conv_wp;
-            if (x >= ep.conv_ow) continue;
-            const size_t pix = (size_t)y * ep.conv_ow + x;
+            size_t pix = n;  // CONV == 3: columns are the output pixels
+            if constexpr (CONV == 1) {
+                const int y = n / ep.conv_wp, x = n - y * ep.conv_wp;
+                if (x >= ep.conv_ow) continue;
+                pix = (size_t)y * ep.conv_ow + x;
+            }
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -765,6 +824,13 @@ hipError_t dispatch_conv(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
     return launch_tile<64, 64, 32, 2, 2, Epi::Store, false, true, 1>(s, g, ep, 1, kps);
 }
 
+// Direct convolution of a CHW image: the 64 x 64 x 32 tile (one pixel and
+// 8 channels per thread in the loader).
+hipError_t dispatch_conv_direct(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
+    if (g.conv_in_c % 32 != 0 || g.k % 32 != 0 || g.k == 0) return hipErrorInvalidValue;
+    return launch_tile<64, 64, 32, 2, 2, Epi::Store, false, true, 3>(s, g, ep, 1, (int)g.k);
+}
+
 // Patch-scatter GEMM (k % 32 == 0): one 64 x 64 x 32 tile shape, since the
 // row count (out_c * kh * kw) and the pixel count are both moderate.
 hipError_t dispatch_scatter(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
@@ -825,6 +891,21 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs &g) {
     ep.rot = g.rot;
     size_t total = g.m * g.n;
     ep.tail_start = total - total % 16;
+    if (g.conv_in_c && g.conv_ih) {
+        if (g.epi != Epi::Store || g.conv_kw == 0 || g.conv_ow == 0 || g.conv_iw == 0 ||
+            g.conv_stride == 0 || g.n % g.conv_ow != 0 || g.k % (g.conv_in_c * g.conv_kw) != 0)
+            return hipErrorInvalidValue;
+        ep.conv_in_c = (int)g.conv_in_c;
+        ep.conv_kw = (int)g.conv_kw;
+        ep.conv_ow = (int)g.conv_ow;
+        ep.conv_plane = g.n;
+        ep.cd_ih = (int)g.conv_ih;
+        ep.cd_iw = (int)g.conv_iw;
+        ep.cd_stride = (int)g.conv_stride;
+        ep.cd_pad = (int)g.conv_pad;
+        ep.cd_relu = g.conv_relu ? 1 : 0;
+        return dispatch_conv_direct(s, g, ep);
+    }
     if (g.conv_in_c) {
         if (g.epi != Epi::Store) return hipErrorInvalidValue;
         if (g.conv_ow == 0 || g.conv_ow > g.conv_wp || g.n % g.conv_wp != 0)

@@ -130,6 +130,13 @@ struct GemmArgs {
     // (bias per output channel; the conv_wp - conv_ow junk columns are not
     // stored).  conv_in_c must be a multiple of 32.
     size_t conv_in_c = 0, conv_kw = 0, conv_wp = 0, conv_ow = 0;
+    // Direct convolution of a CHW image (Store only, set conv_ih): bt is the
+    // image [conv_in_c][conv_ih][conv_iw] itself, n = oh * conv_ow output
+    // pixels, k = kh * conv_kw * conv_in_c (conv_in_c % 32 == 0), stride
+    // conv_stride, zero padding conv_pad, ReLU on the image when conv_relu;
+    // a and c as above (c = CHW [m][oh][conv_ow], no junk columns).
+    size_t conv_ih = 0, conv_iw = 0, conv_stride = 0, conv_pad = 0;
+    bool conv_relu = false;
     // Patch scatter of a kernel == stride transposed convolution (Store
     // only, k % 32 == 0): a is the weight [out_c * kh * kw][k], bt the
     // channel-last input [ih * iw][k] (n = ih * iw), and C[(oc * kh + ky) * kw
