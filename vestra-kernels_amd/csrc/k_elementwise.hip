@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float *__restrict_
                                                         float *__restrict__ out, size_t rows,
                                                         size_t cols, float eps) {
     const int lane = threadIdx.x & 63;
-    size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    size_t row = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= rows) return;
     const float *x = in + row * cols;
     float *y = out + row * cols;
@@ -373,7 +373,9 @@ hipError_t launch_gelu(hipStream_t s, float *v, size_t n) {
 hipError_t launch_layernorm(hipStream_t s, const float *in, const float *gamma,
                             const float *beta, float *out, size_t rows, size_t cols, float eps) {
     if (rows == 0 || cols == 0) return hipSuccess;
-    layernorm_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(in, gamma, beta, out, rows, cols,
+    // Up to 2048 rows, one row per workgroup spreads the rows over every CU.
+    const unsigned wpb = rows <= 2048 ? 1 : 4;  // waves (rows) per workgroup
+    layernorm_kernel<<<(unsigned)((rows + wpb - 1) / wpb), 64 * wpb, 0, s>>>(in, gamma, beta, out, rows, cols,
                                                                 eps);
     return hipGetLastError();
 }

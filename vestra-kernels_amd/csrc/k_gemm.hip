@@ -629,7 +629,7 @@ __global__ __launch_bounds__(256) void splitk_residual_ln_kernel(int M, int N, E
                                                                  float *__restrict__ ln_out,
                                                                  float eps) {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= M) return;
     const int n4 = N >> 2;
     const size_t mn4 = (size_t)M * n4;
@@ -867,12 +867,15 @@ static hipError_t residual_ln(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
         e = run_cfg<Epi::Residual, true>(s, g, ep, t, splits);
     }
     if (e != hipSuccess) return e;
-    const dim3 grid((unsigned)((g.m + 3) / 4));
-    const int m = (int)g.m, n = (int)g.n;
+    // One wave per row; up to 2048 rows, one row per workgroup spreads the
+    // rows over every CU.
+    const unsigned wpb = g.m <= 2048 ? 1 : 4;
+    const dim3 grid((unsigned)((g.m + wpb - 1) / wpb));
+    const int m = (int)g.m, n = (int)g.n, nt = (int)(64 * wpb);
     switch (splits) {
-        case 2: splitk_residual_ln_kernel<2><<<grid, 256, 0, s>>>(m, n, ep, g.ln_gamma, g.ln_beta, g.ln_out, g.ln_eps); break;
-        case 3: splitk_residual_ln_kernel<3><<<grid, 256, 0, s>>>(m, n, ep, g.ln_gamma, g.ln_beta, g.ln_out, g.ln_eps); break;
-        default: splitk_residual_ln_kernel<4><<<grid, 256, 0, s>>>(m, n, ep, g.ln_gamma, g.ln_beta, g.ln_out, g.ln_eps); break;
+        case 2: splitk_residual_ln_kernel<2><<<grid, nt, 0, s>>>(m, n, ep, g.ln_gamma, g.ln_beta, g.ln_out, g.ln_eps); break;
+        case 3: splitk_residual_ln_kernel<3><<<grid, nt, 0, s>>>(m, n, ep, g.ln_gamma, g.ln_beta, g.ln_out, g.ln_eps); break;
+        default: splitk_residual_ln_kernel<4><<<grid, nt, 0, s>>>(m, n, ep, g.ln_gamma, g.ln_beta, g.ln_out, g.ln_eps); break;
     }
     return hipGetLastError();
 }

@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void layernorm_q8_0_kernel(const float *__rest
                                                              uint16_t *__restrict__ dbits,
                                                              int rows, int cols, float eps) {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= rows) return;
     const f32x4 *x = reinterpret_cast<const f32x4 *>(in + (size_t)row * cols);
     const int n4 = cols >> 2;
@@ -494,6 +494,8 @@ hipError_t launch_layernorm_q8_0(hipStream_t s, const float *x, const float *gam
     if (cols % 32 != 0 || cols > 1024 || cols == 0 || rows > (size_t)INT32_MAX / 4 ||
         ((((uintptr_t)x) | ((uintptr_t)gamma) | ((uintptr_t)beta)) & 15) != 0)
         return hipErrorInvalidValue;
+    // Four rows (waves) per workgroup: at 865 rows, one row per workgroup
+    // measured no faster here.
     layernorm_q8_0_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(x, gamma, beta, qs, d,
                                                                      (int)rows, (int)cols, eps);
     return hipGetLastError();
