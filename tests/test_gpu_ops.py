@@ -177,6 +177,40 @@ def test_fc1_gelu_epilogue_vs_oracle(rt):
     assert max_rel(got, exp) <= 1e-5
 
 
+@pytest.mark.parametrize("m,k,n", [(865, 768, 3072), (400, 768, 3072), (865, 768, 3136),
+                                   (300, 256, 4096), (3460, 768, 3072)])
+def test_gemm_balanced_tail(rt, monkeypatch, m, k, n):
+    """The tiles past the last whole round over the CUs run as K pieces that
+    the last piece to finish sums in piece order (64 x 64 tile, GELU
+    epilogue).  Shapes: fc1 (672 tiles, 3 pieces), 336 tiles (3 pieces), 686
+    tiles (4 pieces, tail padded to a multiple of 8), K = 256 (2 pieces), the
+    batched fc1 (2640 tiles, XCD-ordered).  Bars: identical run to run, and
+    within 1e-5 of the one-workgroup-per-tile grid, from which the tail's
+    K-split sums must differ in some bits (the tail ran)."""
+    a = rt.upload_f32(seeded.normal(41 + m, m * k))
+    lin = rt.prepare_linear_f32(k, n, seeded.normal(42, k * n, 0.02), seeded.normal(43, n, 0.02))
+    monkeypatch.setenv("VESTRA_HIP_GEMM_TAIL", "1")
+    got = rt.download_f32(lin.run_gelu(a, m))
+    again = rt.download_f32(lin.run_gelu(a, m))
+    assert_bits_equal(again, got, "balanced tail rerun")
+    monkeypatch.setenv("VESTRA_HIP_GEMM_TAIL", "0")
+    whole = rt.download_f32(lin.run_gelu(a, m))
+    assert max_rel(got, whole) <= 1e-5
+    assert (got.view(np.uint32) != whole.view(np.uint32)).any()
+
+
+def test_gemm_balanced_tail_store_matches_float64(rt):
+    """Store epilogue through the row-major GEMM: 336 tiles, K = 512 in two
+    pieces; the fp32 error bound of test_gemm_row_major_matches_float64."""
+    m, k, n = 400, 512, 3072
+    a = seeded.normal(51, m * k)
+    b = seeded.normal(52, k * n)
+    c = rt.download_f32(rt.gemm_row_major_f32(rt.upload_f32(a), rt.upload_f32(b), m, k, n))
+    ref = a.reshape(m, k).astype(np.float64) @ b.reshape(k, n).astype(np.float64)
+    bound = k * 6e-8 * (np.abs(a.reshape(m, k)).astype(np.float64) @ np.abs(b.reshape(k, n)))
+    assert np.all(np.abs(c.reshape(m, n) - ref) <= bound + 1e-30)
+
+
 def test_residual_epilogue_vs_oracle(rt):
     m, k, n = 865, 3072, 768
     a = seeded.normal(31, m * k)

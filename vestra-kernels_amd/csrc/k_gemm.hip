@@ -52,6 +52,14 @@ struct EpiArgs {
     // [cd_iw] read in place; column n is output pixel (n / conv_ow, n %
     // conv_ow) and the output is c[m * N + n]; ReLU on the image when cd_relu.
     int cd_ih, cd_iw, cd_stride, cd_pad, cd_relu;
+    // Balanced tail (TAIL kernels): tiles [0, tail_full) run whole; each of
+    // the tail_count tiles after them runs as tail_splits K pieces of
+    // tail_kps, whose partials (in `partial`, one [FM][FN][4][threads] block
+    // per piece) the last piece to finish sums in piece order before the
+    // epilogue.  tail_cnt holds one arrival counter per tail tile: zero
+    // between launches (the last piece resets it).
+    int tail_full, tail_splits, tail_count, tail_kps;
+    unsigned *tail_cnt;
 };
 
 // Applies a Store / Gelu / Residual epilogue to one output element.
@@ -78,6 +86,16 @@ __device__ __forceinline__ void epilogue_store(const EpiArgs &ep, size_t idx, in
 // Measured on MI355X this pays for the batched shapes (M = 4 x 865) and costs
 // a little at M = 865, where the GEMMs are not fetch-bound; without
 // xcd_order the tiles follow the launch grid.
+__device__ __forceinline__ void tile_walk(int t, int nx, int ny, int &tm, int &tn) {
+    const int gm = min(8, ny);
+    const int group = t / (gm * nx);
+    const int first = group * gm;
+    const int rows = min(ny - first, gm);
+    const int local = t - group * gm * nx;
+    tm = first + local % rows;
+    tn = local / rows;
+}
+
 __device__ __forceinline__ void tile_of_block(bool xcd_order, int &tm, int &tn, int &z) {
     if (!xcd_order) {
         tm = blockIdx.y;
@@ -92,14 +110,36 @@ __device__ __forceinline__ void tile_of_block(bool xcd_order, int &tm, int &tn, 
     const int pid = x * q + min(x, r) + bid / 8;
     const int per = nx * ny;
     z = pid / per;
-    const int t = pid - z * per;
-    const int gm = min(8, ny);
-    const int group = t / (gm * nx);
-    const int first = group * gm;
-    const int rows = min(ny - first, gm);
-    const int local = t - group * gm * nx;
-    tm = first + local % rows;
-    tn = local / rows;
+    tile_walk(pid - z * per, nx, ny, tm, tn);
+}
+
+// TAIL grids are one-dimensional: workgroups [0, tail_full) take the whole
+// tiles (tail_full % 8 == 0; with xcd_order renumbered as above), and the
+// rest the K pieces of the tail tiles, numbered so that the tail_splits
+// pieces of one tile share bid % 8, i.e. one XCD and its L2.  Tail indices
+// past tail_count (padding to a multiple of 8) return -1.
+__device__ __forceinline__ int tail_tile_of_block(const EpiArgs &ep, bool xcd_order, int nx, int ny,
+                                                  int &tm, int &tn, int &piece, int &u) {
+    const int bid = blockIdx.x;
+    int t;
+    if (bid < ep.tail_full) {
+        piece = -1;
+        u = 0;
+        t = xcd_order ? (bid % 8) * (ep.tail_full / 8) + bid / 8 : bid;
+    } else {
+        const int q = bid - ep.tail_full, r = q / 8;
+        piece = r % ep.tail_splits;
+        u = (r / ep.tail_splits) * 8 + q % 8;
+        if (u >= ep.tail_count) return -1;
+        t = ep.tail_full + u;
+    }
+    if (xcd_order) {
+        tile_walk(t, nx, ny, tm, tn);
+    } else {
+        tm = t / nx;
+        tn = t - tm * nx;
+    }
+    return 0;
 }
 
 // EXACT: K and the split length are multiples of BK and K % 4 == 0, so every
@@ -120,7 +160,8 @@ __device__ __forceinline__ void tile_of_block(bool xcd_order, int &tm, int &tn, 
 // channel; taps outside the image load a clamped in-range pixel and are
 // zeroed when the slice is stored to LDS (after the MFMAs), and the output
 // is the channel-major tile itself, i.e. CHW.
-template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, int CONV = 0>
+template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, int CONV = 0,
+          bool TAIL = false>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__restrict__ A,
                                                               const float *__restrict__ Bt,
                                                               int M, int N, int K,
@@ -146,11 +187,22 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lh = lane >> 4;
     const int wm = wave / WN, wn = wave % WN;
-    int tile_m, tile_n, split;
-    tile_of_block(xcd_order != 0, tile_m, tile_n, split);
+    int tile_m, tile_n, split, kbeg, kend;
+    int piece = -1, tail_u = 0;
+    if constexpr (TAIL) {
+        static_assert(!SPLIT && EXACT && CONV == 0, "balanced tail: plain whole-slice GEMMs");
+        if (tail_tile_of_block(ep, xcd_order != 0, (N + BN - 1) / BN, (M + BM - 1) / BM, tile_m, tile_n,
+                               piece, tail_u) < 0)
+            return;
+        split = 0;
+        kbeg = piece < 0 ? 0 : piece * ep.tail_kps;
+        kend = piece < 0 ? K : kbeg + ep.tail_kps;
+    } else {
+        tile_of_block(xcd_order != 0, tile_m, tile_n, split);
+        kbeg = split * k_per_split;
+        kend = min(K, kbeg + k_per_split);
+    }
     const int m0 = tile_m * BM, n0 = tile_n * BN;
-    const int kbeg = split * k_per_split;
-    const int kend = min(K, kbeg + k_per_split);
     const bool vec = (K & 3) == 0;
 
     // CONV == 3: this thread's pixel (tile column cd_p), channel group and
@@ -353,6 +405,56 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
             compute(cur);
             if (next) lstore(cur ^ 1);
             __syncthreads();
+        }
+    }
+
+    if constexpr (TAIL) {
+        if (piece >= 0) {
+            // Publish this piece's partial (coalesced: consecutive threads,
+            // consecutive floats), then count it in.  Partials are written
+            // and read with device-scope accesses, which bypass the caches
+            // that are not coherent across XCDs, so no cache-wide writeback
+            // or invalidate is needed (an agent-scope fence here costs both,
+            // and doubled the kernel's time).  Every thread waits for its
+            // stores to complete before the barrier, the counter is bumped
+            // after it, and the last piece reads the partials only after
+            // seeing the count.  No piece waits for another, so the grid
+            // drains whatever the residency.
+            __shared__ int tail_last;
+            constexpr int PER = FM * FN * 4;
+            const size_t tile_base = (size_t)tail_u * ep.tail_splits * PER * NT;
+            float *mine = ep.partial + tile_base + (size_t)piece * PER * NT;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        __hip_atomic_store(mine + ((i * FN + j) * 4 + r) * NT + tid, acc[i][j][r],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (tid == 0)
+                tail_last = __hip_atomic_fetch_add(ep.tail_cnt + tail_u, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(ep.tail_splits - 1);
+            __syncthreads();
+            if (!tail_last) return;
+            // The sum in piece order, whichever piece finished last.
+            float *parts = ep.partial + tile_base;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const size_t o = (size_t)((i * FN + j) * 4 + r) * NT + tid;
+                        float v = __hip_atomic_load(parts + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        for (int p = 1; p < ep.tail_splits; p++)
+                            v = v + __hip_atomic_load(parts + (size_t)p * PER * NT + o, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                        acc[i][j][r] = v;
+                    }
+            if (tid == 0) __hip_atomic_store(ep.tail_cnt + tail_u, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 
@@ -767,6 +869,87 @@ void default_tile(const GemmArgs &g, Tile *t, int *splits) {
     }
 }
 
+int cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+struct TailPlan {
+    int full, splits, count;
+};
+
+// Balanced tail for the 64 x 64 x 32 tile.  With T tiles on C CUs the
+// workgroup-per-tile grid ends with a partial round (at M = 865, N = 3072:
+// 672 tiles, 3 on some CUs and 2 on others), and the kernel lasts as long as
+// the busiest CU.  Running the whole rounds as they are and the T % C tiles
+// after them as S pieces of K / S each brings the busiest CU's load from
+// ceil(T / C) tiles to T / C rounded down plus ceil(S (T % C) / C) / S.  S is
+// the smallest of 2..4 with the lowest load (pieces of at least 4 slices).
+// VESTRA_HIP_GEMM_TAIL=0 turns the tail off and =1 takes it whenever it
+// lowers the load at all (A/B studies and tests).
+bool tail_plan(const GemmArgs &g, const Tile &t, TailPlan *plan) {
+    if (t.bm != 64 || t.bn != 64 || t.bk != 32 || t.wm != 2 || t.wn != 2) return false;
+    if (!g.tail_ws || !g.tail_cnt || g.k == 0 || g.k % 32 != 0) return false;
+    const char *env = std::getenv("VESTRA_HIP_GEMM_TAIL");
+    if (env && env[0] == '0') return false;
+    const bool forced = env && env[0] == '1';
+    const long cus = cu_count();
+    if (cus <= 0) return false;
+    const long tiles = (long)((g.m + 63) / 64) * (long)((g.n + 63) / 64);
+    const long full = tiles / cus * cus, rem = tiles - full;
+    const long count8 = (rem + 7) / 8 * 8;
+    if (full == 0 || rem == 0 || full % 8 != 0) return false;
+    const long ktiles = (long)(g.k / 32);
+    // Measured on MI355X (fc1-shaped, N = 3072, K = 768): 2 pieces of the
+    // 128-tile tail at M = 512 and of the 112-tile tail at M = 832 cut the
+    // launch by 9% and 12% (predicted loads -25% and -17%), while 3 pieces at
+    // M = 865 (-11% predicted) made it 5% slower and 3 pieces at M = 3460
+    // (-6%) changed nothing: the pieces' partial traffic and fix-up cost about
+    // a tenth of a round.  Hence a tail only for a predicted cut of 15% or
+    // more, unless forced.
+    const double whole = (double)(full / cus + 1);
+    double best = forced ? whole : whole * 0.85;
+    int pick = 0;
+    for (int sp = 2; sp <= 4; sp++) {
+        if (ktiles % sp != 0 || ktiles / sp < 4) continue;
+        if ((size_t)count8 > g.tail_cnt_n || (size_t)(count8 * sp) * 64 * 64 > g.tail_ws_floats) continue;
+        const double load = (double)(full / cus) + (double)((rem * sp + cus - 1) / cus) / sp;
+        if (load < best) {
+            best = load;
+            pick = sp;
+        }
+    }
+    if (!pick || full + pick * count8 > INT32_MAX) return false;
+    *plan = TailPlan{(int)full, pick, (int)rem};
+    return true;
+}
+
+template <Epi EPI>
+hipError_t launch_tail(hipStream_t s, const GemmArgs &g, EpiArgs ep, const TailPlan &p) {
+    constexpr int BM = 64, BN = 64, BK = 32, WM = 2, WN = 2;
+    constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 4) * sizeof(float);
+    auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, false, true, 0, true>;
+    static std::atomic<uint64_t> configured{0};
+    if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
+    ep.partial = g.tail_ws;
+    ep.tail_cnt = g.tail_cnt;
+    ep.tail_full = p.full;
+    ep.tail_splits = p.splits;
+    ep.tail_count = p.count;
+    ep.tail_kps = (int)g.k / p.splits;
+    const unsigned blocks = (unsigned)(p.full + p.splits * ((p.count + 7) / 8 * 8));
+    const int xcd_order = g.m > 1024;
+    kernel<<<blocks, WM * WN * 64, lds, s>>>(g.a, g.bt, (int)g.m, (int)g.n, (int)g.k, (int)g.k, xcd_order, ep);
+    return hipGetLastError();
+}
+
 template <Epi EPI>
 hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     Tile t;
@@ -774,6 +957,10 @@ hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     if (!tile_override(&t, &splits)) default_tile(g, &t, &splits);
     if (EPI == Epi::Qkv) splits = 1;
     if (splits > 1 && (g.ws == nullptr || g.ws_floats < (size_t)splits * g.m * g.n)) splits = 1;
+    if constexpr (EPI == Epi::Store || EPI == Epi::Gelu) {
+        TailPlan p;
+        if (splits == 1 && tail_plan(g, t, &p)) return launch_tail<EPI>(s, g, ep, p);
+    }
     if (splits == 1) {
         hipError_t e = run_cfg<EPI, false>(s, g, ep, t, 1);
         if (e == hipErrorInvalidValue) {

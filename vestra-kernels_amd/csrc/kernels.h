@@ -115,6 +115,16 @@ struct GemmArgs {
     // split-K workspace (>= splits * m * n floats) or null (no split)
     float *ws;
     size_t ws_floats;
+    // Balanced-tail workspace (Store / Gelu on the 64 x 64 tile): when the
+    // tiles do not divide evenly over the CUs, the tiles past the last whole
+    // round run as K pieces summed by the last piece to finish.  tail_ws holds
+    // their partials (kTailTiles * 4 * 4096 floats), tail_cnt one counter per
+    // tail tile (kTailTiles, zero on entry and on return).  Null: no tail.
+    // Launches sharing one tail_cnt must not overlap in time.
+    float *tail_ws = nullptr;
+    size_t tail_ws_floats = 0;
+    unsigned *tail_cnt = nullptr;
+    size_t tail_cnt_n = 0;
     // Residual only: also write LayerNorm(c) row by row to ln_out (the next
     // sub-layer's input), fused into the split-K reduction when possible.
     const float *ln_gamma = nullptr, *ln_beta = nullptr;
@@ -145,6 +155,9 @@ struct GemmArgs {
     size_t scatter_kh = 0, scatter_kw = 0, scatter_iw = 0;
 };
 hipError_t launch_gemm(hipStream_t s, const GemmArgs &g);
+// Sizes of the balanced-tail workspace (GemmArgs::tail_ws / tail_cnt).
+constexpr size_t kTailTiles = 512;
+constexpr size_t kTailFloats = kTailTiles * 4 * 64 * 64;
 
 // ---- Q8_0 (k_q8.hip) --------------------------------------------------------
 // x [rows][k] -> block-major Q8_0: qs [k/32][rows][32] int8, d [k/32][rows] f16 bits

@@ -89,6 +89,8 @@ struct RtState {
     size_t fw_floats = 0;
     char *aq = nullptr;                         // grow-only Q8_0 activation blocks
     size_t aq_bytes = 0;
+    float *tw = nullptr;                        // balanced-tail GEMM partials
+    unsigned *tcnt = nullptr;                   // and arrival counters (zeroed once)
 
     bool profile = false;
     std::vector<ProfileRec> pending;
@@ -104,6 +106,8 @@ struct RtState {
         if (sk) hipFree(sk);
         if (fw) hipFree(fw);
         if (aq) hipFree(aq);
+        if (tw) hipFree(tw);
+        if (tcnt) hipFree(tcnt);
 
         for (auto &p : pending) {
             hipEventDestroy(p.a);
@@ -367,6 +371,29 @@ vh_status splitk_workspace(RtState &s, size_t m, size_t n, float **out, size_t *
     return VH_OK;
 }
 
+// Balanced-tail workspace of the wide GEMMs, allocated on first use.  The
+// counters are zeroed once here; every launch leaves them zero.
+vh_status tail_workspace(RtState &s, vh::GemmArgs &g) {
+    if (!s.tw) {
+        hipStreamSynchronize(s.stream);
+        hipError_t e = hipMalloc(&s.tw, vh::kTailFloats * sizeof(float));
+        if (e == hipSuccess) e = hipMalloc(&s.tcnt, vh::kTailTiles * sizeof(unsigned));
+        if (e == hipSuccess) e = hipMemset(s.tcnt, 0, vh::kTailTiles * sizeof(unsigned));
+        if (e != hipSuccess) {
+            if (s.tw) hipFree(s.tw);
+            if (s.tcnt) hipFree(s.tcnt);
+            s.tw = nullptr;
+            s.tcnt = nullptr;
+            return fail(VH_ERR_UPLOAD, hip_msg("GEMM tail workspace allocation", e));
+        }
+    }
+    g.tail_ws = s.tw;
+    g.tail_ws_floats = vh::kTailFloats;
+    g.tail_cnt = s.tcnt;
+    g.tail_cnt_n = vh::kTailTiles;
+    return VH_OK;
+}
+
 vh_status flash(RtState &s, const float *q, const float *k, const float *v, float *out,
                 size_t bh, size_t tokens, size_t heads, bool token_major, int8_t *q8_qs = nullptr,
                 uint16_t *q8_d = nullptr, bool *quantized = nullptr) {
@@ -434,6 +461,7 @@ vh_status run_lin(RtState &s, const Lin &L, const float *in, size_t rows, vh::Ep
         g.ln_eps = norm->eps;
     }
     TRY(splitk_workspace(s, rows, L.N, &g.ws, &g.ws_floats));
+    TRY(tail_workspace(s, g));
     return launch(s, name, [&] { return vh::launch_gemm(s.stream, g); });
 }
 
@@ -816,7 +844,8 @@ extern "C" vh_status vh_gemm_row_major_f32(const vh_runtime *rt, const vh_tensor
         g.k = k;
         g.epi = vh::Epi::Store;
         g.c = t->ptr;
-        st = launch(s, "gemm", [&] { return vh::launch_gemm(s.stream, g); });
+        st = tail_workspace(s, g);
+        if (!st) st = launch(s, "gemm", [&] { return vh::launch_gemm(s.stream, g); });
     }
     if (bt) hipFreeAsync(bt, s.stream);
     if (st) {
@@ -1944,6 +1973,7 @@ vh_status gemm_nt(RtState &s, const float *a, const float *bt, const float *bias
     g.c = c;
     g.bias = bias;
     TRY(splitk_workspace(s, rows, cols, &g.ws, &g.ws_floats));
+    TRY(tail_workspace(s, g));
     return launch(s, name, [&] { return vh::launch_gemm(s.stream, g); });
 }
 
