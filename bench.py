@@ -189,7 +189,7 @@ def gpu_elementwise(reps: int = 20) -> dict:
     """The bandwidth-bound kernels; bytes = the algorithmic reads plus writes.
     Two size classes: the encoder's own shapes (LayerNorm and quantisation
     over 4 x 865 tokens, GELU over the batched fc1 output), and sizes where
-    bandwidth rather than launch and first-load latency decides (16-33 Mi
+    bandwidth rather than launch and first-load latency decides (32-50 Mi
     floats).  Each case is timed twice: a burst of `reps` back-to-back
     launches between two HIP events (`us_burst`, which can include host issue
     time for kernels shorter than one call's host cost) and per-launch event
@@ -230,8 +230,11 @@ def gpu_elementwise(reps: int = 20) -> dict:
                 2 * heads * n * HD * 4, "rope2d")
 
     block_shapes = [ln_case(4 * T), gelu_case(4 * T * F), q8_case(4 * T), rope_case(2 * 4 * H, 24, 36)]
-    at_scale = [ln_case(21845), gelu_case(32 * 1024 * 1024), add_case(32 * 1024 * 1024),
-                q8_case(21845), rope_case(2 * 4 * H, 72, 48)]
+    # LayerNorm and quantisation allocate their output on every call (~25-30 us
+    # of host time), so their bandwidth cases are sized for kernels longer
+    # than that: 65536 rows.
+    at_scale = [ln_case(65536), gelu_case(32 * 1024 * 1024), add_case(32 * 1024 * 1024),
+                q8_case(65536), rope_case(2 * 4 * H, 72, 48)]
     out = {}
     for label, cases in (("block_shapes", block_shapes), ("bandwidth_sizes", at_scale)):
         res = {}

@@ -372,13 +372,15 @@ vh_status splitk_workspace(RtState &s, size_t m, size_t n, float **out, size_t *
 }
 
 // Balanced-tail workspace of the wide GEMMs, allocated on first use.  The
-// counters are zeroed once here; every launch leaves them zero.
+// counters are zeroed once here, on the runtime stream (so ahead of the
+// first launch that reads them, which the stream's non-blocking flag would
+// not order after a null-stream memset); every launch leaves them zero.
 vh_status tail_workspace(RtState &s, vh::GemmArgs &g) {
     if (!s.tw) {
         hipStreamSynchronize(s.stream);
         hipError_t e = hipMalloc(&s.tw, vh::kTailFloats * sizeof(float));
         if (e == hipSuccess) e = hipMalloc(&s.tcnt, vh::kTailTiles * sizeof(unsigned));
-        if (e == hipSuccess) e = hipMemset(s.tcnt, 0, vh::kTailTiles * sizeof(unsigned));
+        if (e == hipSuccess) e = hipMemsetAsync(s.tcnt, 0, vh::kTailTiles * sizeof(unsigned), s.stream);
         if (e != hipSuccess) {
             if (s.tw) hipFree(s.tw);
             if (s.tcnt) hipFree(s.tcnt);
