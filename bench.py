@@ -33,6 +33,8 @@ sys.path.insert(0, str(ROOT / "vestra-kernels_amd"))
 
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+# Non-packed fp32 VALU lane-ops per second: 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz.
+PEAK_VALU_OPS = 256 * 4 * 16 * 2.4e9
 
 T = 865
 D, H, HD, F = 768, 12, 64, 3072
@@ -177,11 +179,19 @@ def gpu_q8_0(steps: int) -> dict:
     gemm_bytes = m * k + m * (k // 32) * 2 + n * k + n * (k // 32) * 2 + m * n * 4
     quant_bytes = m * k * 4 + m * k + m * (k // 32) * 2
     gbs = gemm_bytes / (g_us * 1e-6) / 1e9
-    log(f"  q8_0 quantize {q_us:.2f} us, gemm {g_us:.2f} us ({gbs:.0f} GB/s algorithmic)")
+    # The bit-exact fold acc + (da * db) * isum is four VALU ops per output
+    # and 32-wide block (int-to-float conversion, two multiplies, add): a
+    # floor the HBM roofline does not see.
+    fold_ops = m * n * (k // 32) * 4
+    valu_us = fold_ops / PEAK_VALU_OPS * 1e6
+    log(f"  q8_0 quantize {q_us:.2f} us, gemm {g_us:.2f} us ({gbs:.0f} GB/s algorithmic, "
+        f"fold VALU floor {valu_us:.2f} us)")
     return {"workload": "q8_0_fc1_865", "quantize_us": round(q_us, 3), "gemm_us": round(g_us, 3),
             "gemm_top_s": round(2.0 * m * n * k / (g_us * 1e-6) / 1e12, 1),
             "gemm_algorithmic_bytes": gemm_bytes, "gemm_gbs": round(gbs, 1),
-            "gemm_frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "quantize_algorithmic_bytes": quant_bytes,
+            "gemm_frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+            "gemm_fold_valu_ops": fold_ops, "gemm_valu_floor_us": round(valu_us, 3),
+            "gemm_frac_valu": round(valu_us / g_us, 4), "quantize_algorithmic_bytes": quant_bytes,
             "quantize_gbs": round(quant_bytes / (q_us * 1e-6) / 1e9, 1)}
 
 
