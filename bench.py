@@ -199,8 +199,10 @@ def gpu_elementwise(reps: int = 20) -> dict:
     """The bandwidth-bound kernels; bytes = the algorithmic reads plus writes.
     Two size classes: the encoder's own shapes (LayerNorm and quantisation
     over 4 x 865 tokens, GELU over the batched fc1 output), and sizes where
-    bandwidth rather than launch and first-load latency decides (32-50 Mi
-    floats).  Each case is timed twice: a burst of `reps` back-to-back
+    HBM bandwidth decides: working sets of 384-768 MiB, past the 256 MiB
+    Infinity Cache that would otherwise serve repeated launches.  A device
+    copy of 256 MiB (hipMemcpyAsync) at the same scale gives the bandwidth a
+    streaming kernel can reach (`frac_copy`).  Each case is timed twice: a burst of `reps` back-to-back
     launches between two HIP events (`us_burst`, which can include host issue
     time for kernels shorter than one call's host cost) and per-launch event
     pairs (`us_event`, each carrying the events' own ~1-2 us).  Both are upper
@@ -213,13 +215,18 @@ def gpu_elementwise(reps: int = 20) -> dict:
     b = rt.upload_f32(np.zeros(D, np.float32))
     cases = []
 
+    def big(seed, n):
+        # Large inputs tile one seeded block of 8 Mi values.
+        base = seeded.normal(seed, min(n, 8 << 20))
+        return np.tile(base, (n + base.size - 1) // base.size)[:n]
+
     def ln_case(rows):
-        x = rt.upload_f32(seeded.normal(31, rows * D))
+        x = rt.upload_f32(big(31, rows * D))
         return (f"layernorm {rows}x{D}", lambda: rt.layernorm_f32(x, g, b, rows, D, 1e-6),
                 2 * rows * D * 4 + 2 * D * 4, "layernorm")
 
     def gelu_case(n):
-        f = rt.upload_f32(seeded.normal(32, n))
+        f = rt.upload_f32(big(32, n))
         return (f"gelu {n}", lambda: rt.gelu_f32_in_place(f), 2 * n * 4, "gelu")
 
     def add_case(n):
@@ -227,25 +234,28 @@ def gpu_elementwise(reps: int = 20) -> dict:
         return (f"add {n}", lambda: rt.add_f32_in_place(a1, a2), 3 * n * 4, "add")
 
     def q8_case(rows):
-        x = rt.upload_f32(seeded.normal(33, rows * D))
+        x = rt.upload_f32(big(33, rows * D))
         return (f"quantize_q8_0 {rows}x{D}", lambda: rt.quantize_q8_0(x, rows, D),
                 rows * D * 4 + rows * D + rows * D // 16, "quantize_q8_0")
 
     def rope_case(heads, grid_h, grid_w):
         n = grid_h * grid_w + 1
-        x = rt.upload_f32(seeded.normal(34, heads * n * HD))
+        x = rt.upload_f32(big(34, heads * n * HD))
         pos = da3.positions_yx(grid_h, grid_w)
         return (f"rope2d {heads}x{n}x{HD}",
                 lambda: rt.rope2d_f32_in_place(x, heads, n, HD, pos, da3.ROPE_FREQ),
                 2 * heads * n * HD * 4, "rope2d")
 
     block_shapes = [ln_case(4 * T), gelu_case(4 * T * F), q8_case(4 * T), rope_case(2 * 4 * H, 24, 36)]
-    # LayerNorm and quantisation allocate their output on every call (~25-30 us
-    # of host time), so their bandwidth cases are sized for kernels longer
-    # than that: 65536 rows.
-    at_scale = [ln_case(65536), gelu_case(32 * 1024 * 1024), add_case(32 * 1024 * 1024),
-                q8_case(65536), rope_case(2 * 4 * H, 72, 48)]
+    def copy_case(n):
+        src, dst = rt.upload_f32(np.ones(n, np.float32)), rt.upload_f32(np.zeros(n, np.float32))
+        return (f"copy {n}", lambda: rt.copy_segment_into_f32(dst, 0, src, 0, n), 2 * n * 4,
+                "copy_segment_into")
+
+    at_scale = [copy_case(64 << 20), ln_case(131072), gelu_case(96 << 20), add_case(64 << 20),
+                q8_case(131072), rope_case(40 * H, 72, 48)]
     out = {}
+    copy_gbs = None  # set by the first bandwidth case, the copy
     for label, cases in (("block_shapes", block_shapes), ("bandwidth_sizes", at_scale)):
         res = {}
         for name, fn, nbytes, prof_name in cases:
@@ -268,6 +278,10 @@ def gpu_elementwise(reps: int = 20) -> dict:
             res[name] = {"us": round(us, 2), "us_burst": round(us_burst, 2),
                          "us_event": round(us_event, 2), "gbs": round(gbs, 1),
                          "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes}
+            if label == "bandwidth_sizes":
+                if prof_name == "copy_segment_into":
+                    copy_gbs = gbs
+                res[name]["frac_copy"] = round(gbs / copy_gbs, 4)
             log(f"  {name:28s} {us:8.2f} us {gbs:8.1f} GB/s "
                 f"(burst {us_burst:.2f}, per-launch events {us_event:.2f})")
         out[label] = res
