@@ -1059,6 +1059,20 @@ static void linear_avx512(size_t m, size_t n, size_t k, const float *a, const fl
     }
 }
 
+/* linear_bias_scale_avx512_rows<6> (src/specialized.rs:880-929), the default
+ * out-proj / fc2 schedule: one task per 6-row tile, each walking every
+ * 64-column panel.  Per output the arithmetic is the column split's. */
+static void linear_avx512_rows(size_t m, size_t n, size_t k, const float *a, const float *b,
+                               int mode, const float *bias, const float *scale, float *c) {
+    size_t tiles = (m + 5) / 6;
+#pragma omp parallel for OMP_THREADS schedule(dynamic, 1)
+    for (size_t t = 0; t < tiles; t++) {
+        size_t row0 = t * 6, rows = m - row0 < 6 ? m - row0 : 6;
+        for (size_t col0 = 0; col0 < n; col0 += 64)
+            tile_6x64(rows, k, n, a + row0 * k, b, col0, mode, bias, scale, c + row0 * n + col0, n);
+    }
+}
+
 static void linear_scalar_epilogue(size_t m, size_t n, size_t k, const float *a, const float *b,
                                    int mode, const float *bias, const float *scale, float *c) {
     vko_linear_fma_scalar(m, n, k, a, b, c);
@@ -1084,7 +1098,7 @@ void vko_linear(size_t m, size_t n, size_t k, const float *a, const float *b, fl
 void vko_linear_bias_scale(size_t m, size_t n, size_t k, const float *a, const float *b,
                            const float *bias, const float *scale, float *c) {
     if (has_avx512f_fma() && n % 64 == 0)
-        linear_avx512(m, n, k, a, b, 2, bias, scale, c);
+        linear_avx512_rows(m, n, k, a, b, 2, bias, scale, c);
     else
         linear_scalar_epilogue(m, n, k, a, b, 2, bias, scale, c);
 }

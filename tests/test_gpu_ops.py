@@ -151,9 +151,17 @@ def test_gemm_row_major_matches_float64(rt, m, k, n):
     assert np.all(np.abs(c.reshape(m, n) - ref) <= bound + 1e-30)
 
 
-@pytest.mark.parametrize("k,n", [(768, 2304), (768, 768), (768, 3072), (3072, 768)])
-def test_da3_projection_shapes_vs_oracle(rt, k, n):
-    m = 865
+# M = 865 is one 504x336 image; 3460 = the batch of 4 (BASELINE config 5a) and
+# 3457 = one 1008x672 image (config 5b).  Past M = 1024 the GEMM takes other
+# tiles, an XCD-ordered tile walk and other split-K choices, so those paths
+# are compared with the oracle at those sizes too.
+PROJ_M = [865, 3460, 3457]
+PROJ_KN = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
+
+
+@pytest.mark.parametrize("m", PROJ_M)
+@pytest.mark.parametrize("k,n", PROJ_KN)
+def test_da3_projection_shapes_vs_oracle(rt, m, k, n):
     a = seeded.normal(11, m * k)
     w = seeded.normal(12, k * n, 0.02)
     bias = seeded.normal(13, n, 0.01)
@@ -162,10 +170,15 @@ def test_da3_projection_shapes_vs_oracle(rt, k, n):
     lin = rt.prepare_linear_f32(k, n, w, bias, scale)
     got = rt.download_f32(lin.run(rt.upload_f32(a), m))
     assert max_rel(got, exp) <= 1e-5
+    # a transposed weight (a plausible packing mistake) misses by far more
+    if k == n:
+        wt = np.ascontiguousarray(w.reshape(k, n).T).reshape(-1)
+        assert max_rel(O.linear_bias_scale(a, wt, bias, scale, m, n, k), exp) >= 1e-3
 
 
-def test_fc1_gelu_epilogue_vs_oracle(rt):
-    m, k, n = 865, 768, 3072
+@pytest.mark.parametrize("m", PROJ_M)
+def test_fc1_gelu_epilogue_vs_oracle(rt, m):
+    k, n = 768, 3072
     a = seeded.normal(21, m * k)
     w = seeded.normal(22, k * n, 0.02)
     bias = seeded.normal(23, n, 0.02)
@@ -211,12 +224,14 @@ def test_gemm_balanced_tail_store_matches_float64(rt):
     assert np.all(np.abs(c.reshape(m, n) - ref) <= bound + 1e-30)
 
 
-def test_residual_epilogue_vs_oracle(rt):
-    m, k, n = 865, 3072, 768
+@pytest.mark.parametrize("m", PROJ_M)
+@pytest.mark.parametrize("k", [768, 3072], ids=["proj", "fc2"])
+def test_residual_epilogue_vs_oracle(rt, m, k):
+    n = 768
     a = seeded.normal(31, m * k)
     w = seeded.normal(32, k * n, 0.02)
     bias = seeded.normal(33, n, 0.02)
-    ls = np.full(n, 0.5, np.float32)
+    ls = (0.1 + 0.9 * seeded.uniform01(35, n)).astype(np.float32)
     x = seeded.normal(34, m * n)
     y = O.linear_bias_scale(a, w, bias, ls, m, n, k)
     exp = O.kernels_add(x, y)
@@ -227,21 +242,35 @@ def test_residual_epilogue_vs_oracle(rt):
     assert max_rel(rt.download_f32(xt), exp) <= 1e-5
 
 
-@pytest.mark.parametrize("rope", [False, True])
-def test_qkv_head_major_rope_vs_oracle(rt, rope):
-    T = 865
-    a = seeded.normal(41, T * 768)
+@pytest.mark.parametrize("images, rows, cols, rope", [
+    (1, 24, 36, False), (1, 24, 36, True), (4, 24, 36, True), (1, 48, 72, True)],
+    ids=["865", "865-rope", "4x865-rope", "3457-rope"])
+def test_qkv_head_major_rope_vs_oracle(rt, images, rows, cols, rope):
+    """Q/K/V head-major [images][12][tokens][64] with bias, and the 2-D RoPE on
+    the 24 x 36 grid (one image and the batch of 4, M = 3460) and on the
+    48 x 72 grid of a 1008x672 image (M = 3457)."""
+    T = rows * cols + 1
+    a = seeded.normal(41, images * T * 768)
     w = seeded.normal(42, 768 * 2304, 0.02)
     bias = seeded.normal(43, 2304, 0.02)
-    pos = da3.positions_yx(24, 36)
-    eq, ek, ev = O.qkv(a, w, bias, T)
-    if rope:
-        eq = O.rope2d(eq, 12, T, 64, pos, 100.0)
-        ek = O.rope2d(ek, 12, T, 64, pos, 100.0)
+    pos = da3.positions_yx(rows, cols)
+    exp = {"q": [], "k": [], "v": []}
+    for img in range(images):
+        eq, ek, ev = O.qkv(a[img * T * 768:(img + 1) * T * 768], w, bias, T)
+        if rope:
+            eq = O.rope2d(eq, 12, T, 64, pos, 100.0)
+            ek = O.rope2d(ek, 12, T, 64, pos, 100.0)
+        for name, e in (("q", eq), ("k", ek), ("v", ev)):
+            exp[name].append(e)
     lin = rt.prepare_linear_f32(768, 2304, w, bias)
-    q, k, v = lin.run_qkv_hnd(rt.upload_f32(a), 1, T, 12, pos if rope else None, 100.0)
-    for got, exp, name in ((q, eq, "q"), (k, ek, "k"), (v, ev, "v")):
-        assert max_rel(rt.download_f32(got), exp) <= 1e-5, name
+    q, k, v = lin.run_qkv_hnd(rt.upload_f32(a), images, T, 12, pos if rope else None, 100.0)
+    for got, name in ((q, "q"), (k, "k"), (v, "v")):
+        e = np.concatenate(exp[name])
+        g = rt.download_f32(got)
+        assert max_rel(g, e) <= 1e-5, name
+        for img in range(images):  # every image in its own slot, not just overall
+            sl = slice(img * T * 768, (img + 1) * T * 768)
+            assert max_rel(g[sl], e[sl]) <= 1e-5, (name, img)
 
 
 # ---- attention ---------------------------------------------------------------
@@ -256,6 +285,25 @@ def test_online_attention_matches_naive_cases(rt, heads, n, hd, seed):
     got = rt.download_f32(rt.attention_online_f32(rt.upload_f32(q), rt.upload_f32(k),
                                                   rt.upload_f32(v), heads, n, hd))
     assert np.abs(got - exp).max() < 1e-4
+
+
+@pytest.mark.parametrize("heads,n,hd", [(3, 1, 5), (2, 300, 7), (5, 865, 40), (1, 1000, 63),
+                                        (12, 200, 1)])
+def test_online_attention_small_head_dims_vs_naive(rt, heads, n, hd):
+    """Head dims below 64 run the MFMA flash kernel on rows zero-padded to 64
+    with a 1/sqrt(hd) scale: odd widths (the pad and unpad handle a partial
+    float4), one token, and sequences long enough for key splits.  N(0,1)
+    inputs; bar 1e-4 max-relative against attention_naive, which a scale of
+    1/8 instead of 1/sqrt(hd) misses."""
+    q, k, v = (seeded.normal(600 + i, heads * n * hd) for i in range(3))
+    exp = O.attention_naive(q, k, v, heads, n, hd)
+    got = rt.download_f32(rt.attention_online_f32(rt.upload_f32(q), rt.upload_f32(k),
+                                                  rt.upload_f32(v), heads, n, hd))
+    assert got.shape == exp.shape
+    assert max_rel(got, exp) <= 1e-4
+    if n > 1 and hd != 64:
+        wrong = O.attention_naive(q * np.float32(np.sqrt(hd) / 8.0), k, v, heads, n, hd)
+        assert max_rel(wrong, exp) >= 1e-2
 
 
 def test_flash_da3_production_shape_vs_oracle(rt):

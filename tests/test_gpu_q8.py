@@ -24,7 +24,7 @@ from vestra_hip import da3, seeded
 pytestmark = pytest.mark.gpu
 
 BLOCK_TOL = 1e-4
-ENCODER_TOL = 1e-3
+MIXED_TOL = 2e-2  # f32/Q8_0 encoder at O(1) LayerScale (quantisation-step flips)
 
 
 def _linear_case(rt, rows, k, n, seed, gamma):
@@ -158,11 +158,16 @@ def test_q8_block_batched_images(rt):
 def test_encoder_mixing_f32_and_q8_blocks(rt):
     """An f32 block's fc2 writes the next block's LayerNorm1 input; a Q8_0
     block's does not, so the block after it normalises its own input.  The
-    fused encoder run equals block-by-block runs bit for bit and stays within
-    the encoder bar of the oracle."""
+    fused encoder run equals block-by-block runs bit for bit.  Against the
+    oracle, LayerScale is drawn per channel from U(0.1, 1) so that every
+    branch moves the output.  The bar is 2e-2: where the device's LayerNorm
+    or attention rounds an activation across a quantisation step, a Q8_0
+    GEMM output moves by d_a*d_b*q_b, and perturbing the oracle's input by
+    1e-7 relative already moves this 4-layer output by 2.2e-3.  An encoder
+    that returns its input misses that bar by more than 10x."""
     T, images = 865, 1
     q8 = [False, True, True, False]
-    ws = [da3.block_weights(seed=45, layer=l) for l in range(len(q8))]
+    ws = [da3.block_weights(seed=45, layer=l, layerscale="uniform") for l in range(len(q8))]
     x = seeded.normal(4500, images * T * 768)
     pos = da3.positions_yx(24, 36)
     blocks = [rt.prepare_block(w, q8_0=q) for w, q in zip(ws, q8)]
@@ -174,4 +179,5 @@ def test_encoder_mixing_f32_and_q8_blocks(rt):
         rt.vit_block_run(b, step, images, T, pos)
     assert_bits_equal(got, rt.download_f32(step), "fused vs block by block")
     exp = O.encoder(x, ws, images, T, pos, q8_0=q8)
-    assert max_rel(got, exp) <= ENCODER_TOL
+    assert max_rel(got, exp) <= MIXED_TOL
+    assert max_rel(x, exp) >= 10 * MIXED_TOL

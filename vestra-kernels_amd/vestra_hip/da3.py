@@ -55,15 +55,24 @@ def positions_global(rows: int, cols: int, special: int = 1) -> np.ndarray:
     return pos.reshape(-1)
 
 
-def block_weights(seed: int, layer: int = 0, layerscale: float = LAYERSCALE,
+def block_weights(seed: int, layer: int = 0, layerscale: float | str = LAYERSCALE,
                   w_std: float = 0.02, b_std: float = 0.02,
                   qk_norm: bool = False) -> dict[str, np.ndarray]:
     """Seeded block parameters: weights N(0, w_std^2) row-major [in, out],
-    biases N(0, b_std^2), LayerNorm gamma=1 / beta=0, LayerScale constant.
+    biases N(0, b_std^2), LayerNorm gamma=1 / beta=0, LayerScale constant,
+    or, with layerscale="uniform", drawn per channel from U(0.1, 1) (large
+    enough that every branch moves the residual stream well past f32
+    rounding, so an encoder's output checks each layer's arithmetic).
     With qk_norm (DA3's late blocks) the 64-wide Q and K LayerNorms get
     gamma ~ 1 + N(0, 0.1^2) and beta ~ N(0, b_std^2)."""
     def n(tid, count, std):
         return seeded.normal(seeded.tensor_seed(seed, layer, tid), count, std)
+
+    def ls(tid):
+        if layerscale == "uniform":
+            u = seeded.uniform01(seeded.tensor_seed(seed, layer, tid), DIM)
+            return (0.1 + 0.9 * u).astype(np.float32)
+        return np.full(DIM, layerscale, np.float32)
 
     extra = {}
     if qk_norm:
@@ -80,12 +89,12 @@ def block_weights(seed: int, layer: int = 0, layerscale: float = LAYERSCALE,
         "b_qkv": n(2, QKV, b_std),
         "w_proj": n(3, DIM * DIM, w_std),
         "b_proj": n(4, DIM, b_std),
-        "ls1": np.full(DIM, layerscale, np.float32),
+        "ls1": ls(20),
         "ln2_gamma": np.ones(DIM, np.float32),
         "ln2_beta": np.zeros(DIM, np.float32),
         "w_fc1": n(5, DIM * MLP, w_std),
         "b_fc1": n(6, MLP, b_std),
         "w_fc2": n(7, MLP * DIM, w_std),
         "b_fc2": n(8, DIM, b_std),
-        "ls2": np.full(DIM, layerscale, np.float32),
+        "ls2": ls(21),
     }
