@@ -21,8 +21,12 @@
 // is the default for one-stream layouts, flash_kernel serves two-stream
 // layouts.
 //
-// attention_online_kernel: the reference device kernel's contract
-// (src/cuda.rs:153-194): any head_dim <= 64, one thread per (head, query).
+// Head dims below 64 (the generic online-attention contract of
+// src/cuda.rs:868-922) run through the same MFMA kernel: pad_rows64_kernel
+// widens Q, K and V rows to 64 with zeros (the zero dims add nothing to a
+// score and give zero output columns), the softmax takes a runtime scale of
+// 1/sqrt(head_dim), and unpad_rows_kernel keeps the first head_dim columns.
+#include <algorithm>
 #include <cstdlib>
 
 #include "common.h"
@@ -44,6 +48,7 @@ struct FlashArgs {
     int xcd_map;  // 1: place all q-tiles of a head on one XCD's L2
     // Key split across workgroups: split z takes keys [z*split_keys, ...).
     int splits, split_keys;
+    float scale_log2;  // softmax scale times log2(e): 1/8 * log2(e) for DA3
     float *po;    // [splits][bh][T][64] unnormalised outputs
     float2 *pml;  // [splits][bh][T] (running max in the base-2 domain, sum)
     // Token-major split runs only: when q8_qs is set, the merge writes the
@@ -148,7 +153,7 @@ __global__ __launch_bounds__(256 * KVS) __attribute__((amdgpu_waves_per_eu(1, 2)
         }
     };
 
-    const float scale = 0.125f * kLog2e;
+    const float scale = fa.scale_log2;
     float m = -INFINITY;  // running max (base-2 domain) of this lane's query
     float l = 0.0f;       // partial running sum over this lane's keys
     f32x4 o[4];           // o[df][r] = O[query][16*df + 4*lh + r] (unnormalised)
@@ -404,7 +409,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     };
 
-    const float scale = 0.125f * kLog2e;
+    const float scale = fa.scale_log2;
     float m = -INFINITY;  // running max (base 2) of query li
     float l = 0.0f;       // partial running sum over this lane's keys
     f32x4 o[4];           // o[df][r] = O[query qw + 4lh + r][4li + df] (unnormalised)
@@ -642,44 +647,42 @@ hipError_t run_flash_direct(hipStream_t s, const FlashArgs &fa) {
     return hipGetLastError();
 }
 
-// src/cuda.rs:153-194 contract: one thread per (head, query), 64-key tiles.
-__global__ void attention_online_kernel(const float *__restrict__ q, const float *__restrict__ k,
-                                        const float *__restrict__ v, float *__restrict__ out,
-                                        int tokens, int hd, float scale, int rows) {
-    int row = blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= rows) return;
-    const int head = row / tokens, query = row % tokens;
-    const size_t base = (size_t)head * tokens * hd;
-    const float *qi = q + base + (size_t)query * hd;
-    float acc[64];
-    for (int d = 0; d < 64; d++) acc[d] = 0.0f;
-    float mrun = -INFINITY, lsum = 0.0f;
-    for (int j0 = 0; j0 < tokens; j0 += 64) {
-        int j1 = min(j0 + 64, tokens);
-        float sc[64];
-        float tmax = -INFINITY;
-        for (int j = j0; j < j1; j++) {
-            const float *kj = k + base + (size_t)j * hd;
-            float dot = 0.0f;
-            for (int d = 0; d < hd; d++) dot += qi[d] * kj[d];
-            sc[j - j0] = dot * scale;
-            tmax = fmaxf(tmax, sc[j - j0]);
-        }
-        float mnew = fmaxf(mrun, tmax);
-        float corr = isfinite(mrun) ? expf(mrun - mnew) : 0.0f;
-        lsum *= corr;
-        for (int d = 0; d < hd; d++) acc[d] *= corr;
-        for (int j = j0; j < j1; j++) {
-            float pv = expf(sc[j - j0] - mnew);
-            lsum += pv;
-            const float *vj = v + base + (size_t)j * hd;
-            for (int d = 0; d < hd; d++) acc[d] += pv * vj[d];
-        }
-        mrun = mnew;
+// Rows of hd < 64 floats widened to 64 (zeros past hd); blockIdx.y picks
+// one of the three operands, a thread writes one float4 of a padded row.
+__global__ __launch_bounds__(256) void pad_rows64_kernel(const float *__restrict__ q,
+                                                         const float *__restrict__ k,
+                                                         const float *__restrict__ v,
+                                                         float *__restrict__ pq,
+                                                         float *__restrict__ pk,
+                                                         float *__restrict__ pv, size_t rows,
+                                                         int hd) {
+    const float *src = blockIdx.y == 0 ? q : (blockIdx.y == 1 ? k : v);
+    float *dst = blockIdx.y == 0 ? pq : (blockIdx.y == 1 ? pk : pv);
+    const size_t n = rows * 16;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const size_t row = i >> 4;
+        const int d0 = (int)(i & 15) * 4;
+        const float *sr = src + row * hd;
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[e] = d0 + e < hd ? sr[d0 + e] : 0.0f;
+        *reinterpret_cast<f32x4 *>(dst + row * D + d0) = o;
     }
-    float *oi = out + base + (size_t)query * hd;
-    float inv = 1.0f / lsum;
-    for (int d = 0; d < hd; d++) oi[d] = acc[d] * inv;
+}
+
+// The first hd columns of 64-wide rows, packed into hd-wide rows.
+__global__ __launch_bounds__(256) void unpad_rows_kernel(const float *__restrict__ src,
+                                                         float *__restrict__ dst, size_t rows,
+                                                         int hd) {
+    const size_t n = rows * hd;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const size_t row = i / hd;
+        dst[i] = src[row * D + (i - row * hd)];
+    }
+}
+
+unsigned stride_grid(size_t threads) {
+    return (unsigned)std::min<size_t>((threads + 255) / 256, 16384);
 }
 
 }  // namespace
@@ -691,10 +694,11 @@ size_t flash_workspace_floats(size_t bh, size_t tokens) {
 hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k, const float *v,
                                   float *out, size_t bh, size_t tokens, size_t heads,
                                   bool token_major, float *ws, size_t ws_floats, int8_t *q8_qs,
-                                  uint16_t *q8_d, bool *quantized) {
+                                  uint16_t *q8_d, bool *quantized, float softmax_scale) {
     if (quantized) *quantized = false;
     if (bh == 0 || tokens == 0) return hipSuccess;
     FlashArgs fa{};
+    fa.scale_log2 = softmax_scale * kLog2e;
     fa.q = q;
     fa.k = k;
     fa.v = v;
@@ -771,13 +775,17 @@ hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k,
     return token_major ? run_flash<true, 1, false>(s, fa) : run_flash<false, 1, false>(s, fa);
 }
 
-hipError_t launch_attention_online(hipStream_t s, const float *q, const float *k,
-                                   const float *v, float *out, size_t heads, size_t tokens,
-                                   size_t head_dim, float scale) {
-    size_t rows = heads * tokens;
+hipError_t launch_pad_rows64(hipStream_t s, const float *q, const float *k, const float *v,
+                             float *pq, float *pk, float *pv, size_t rows, size_t hd) {
     if (rows == 0) return hipSuccess;
-    attention_online_kernel<<<(unsigned)((rows + 63) / 64), 64, 0, s>>>(
-        q, k, v, out, (int)tokens, (int)head_dim, scale, (int)rows);
+    pad_rows64_kernel<<<dim3(stride_grid(rows * 16), 3), 256, 0, s>>>(q, k, v, pq, pk, pv, rows,
+                                                                     (int)hd);
+    return hipGetLastError();
+}
+
+hipError_t launch_unpad_rows(hipStream_t s, const float *src, float *dst, size_t rows, size_t hd) {
+    if (rows == 0) return hipSuccess;
+    unpad_rows_kernel<<<stride_grid(rows * hd), 256, 0, s>>>(src, dst, rows, (int)hd);
     return hipGetLastError();
 }
 

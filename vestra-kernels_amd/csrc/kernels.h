@@ -44,12 +44,14 @@ hipError_t launch_transpose(hipStream_t s, const float *in, float *out, size_t r
                             size_t cols);
 
 // ---- attention (k_attention.hip) ----------------------------------------
-// Generic online softmax for head_dim <= 64 (the reference device oracle's
-// contract), one thread per (head, query).
-hipError_t launch_attention_online(hipStream_t s, const float *q, const float *k,
-                                   const float *v, float *out, size_t heads, size_t tokens,
-                                   size_t head_dim, float scale);
-// fp32-MFMA flash attention, head_dim 64, scale 1/8.  q/k/v [bh][tokens][64]
+// Head dims below 64 through the flash kernel: q/k/v rows of hd floats
+// widened to 64 with zeros (pq/pk/pv [rows][64]), and the first hd columns
+// of [rows][64] packed back into [rows][hd].
+hipError_t launch_pad_rows64(hipStream_t s, const float *q, const float *k, const float *v,
+                             float *pq, float *pk, float *pv, size_t rows, size_t hd);
+hipError_t launch_unpad_rows(hipStream_t s, const float *src, float *dst, size_t rows, size_t hd);
+// fp32-MFMA flash attention, head_dim 64, softmax scale 1/8 by default
+// (1/sqrt(hd) for zero-padded rows of hd < 64).  q/k/v [bh][tokens][64]
 // with bh = images*heads; out head-major or token-major [img][tokens][heads*64].
 // Key splits across workgroups need a workspace of flash_workspace_floats()
 // floats; with ws == nullptr (or too small) the kernel runs unsplit.
@@ -63,7 +65,7 @@ hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k,
                                   float *out, size_t bh, size_t tokens, size_t heads,
                                   bool token_major, float *ws, size_t ws_floats,
                                   int8_t *q8_qs = nullptr, uint16_t *q8_d = nullptr,
-                                  bool *quantized = nullptr);
+                                  bool *quantized = nullptr, float softmax_scale = 0.125f);
 
 // ---- DPT head (k_dpt.hip) ------------------------------------------------
 // colT [oh*ow][in_c*kh*kw] of a CHW input (zero padding; ReLU on the input

@@ -396,9 +396,18 @@ vh_status tail_workspace(RtState &s, vh::GemmArgs &g) {
     return VH_OK;
 }
 
+// The flash grid holds heads * ceil(tokens/64) * splits workgroups of 256
+// threads; its thread count must fit the 32-bit launch limit.
+bool flash_grid_fits(size_t heads, size_t tokens) {
+    const size_t qtiles = (tokens + 63) / 64;
+    size_t items = 0;
+    return !__builtin_mul_overflow(heads, qtiles, &items) &&
+           items <= (size_t)UINT32_MAX / 256 / vh::kMaxFlashSplits;
+}
+
 vh_status flash(RtState &s, const float *q, const float *k, const float *v, float *out,
                 size_t bh, size_t tokens, size_t heads, bool token_major, int8_t *q8_qs = nullptr,
-                uint16_t *q8_d = nullptr, bool *quantized = nullptr) {
+                uint16_t *q8_d = nullptr, bool *quantized = nullptr, float scale = 0.125f) {
     // Partials of the key splits; without them the kernel runs unsplit.
     const size_t need = vh::flash_workspace_floats(bh, tokens);
     if (s.fw_floats < need) {
@@ -411,7 +420,7 @@ vh_status flash(RtState &s, const float *q, const float *k, const float *v, floa
     }
     return launch(s, "flash_attention", [&] {
         return vh::launch_flash_attention(s.stream, q, k, v, out, bh, tokens, heads, token_major,
-                                          s.fw, s.fw_floats, q8_qs, q8_d, quantized);
+                                          s.fw, s.fw_floats, q8_qs, q8_d, quantized, scale);
     });
 }
 
@@ -954,8 +963,8 @@ extern "C" vh_status vh_attention_online_f32(const vh_runtime *rt, const vh_tens
     if (mul_overflows(heads, tokens, &ht) || mul_overflows(ht, head_dim, &expected) ||
         q->len != expected || k->len != expected || v->len != expected)
         return mismatch(q->len, expected, "vh_attention_online_f32");
-    if (tokens > INT32_MAX || ht > INT32_MAX)
-        return fail(VH_ERR_KERNEL, "attention rows exceed 2^31-1");
+    if (tokens > INT32_MAX || ht > INT32_MAX || !flash_grid_fits(heads, tokens))
+        return fail(VH_ERR_KERNEL, "attention shape exceeds the launch grid");
     GUARD_BEGIN
     RtState &s = *rt->s;
     TRY(set_device(s));
@@ -965,11 +974,26 @@ extern "C" vh_status vh_attention_online_f32(const vh_runtime *rt, const vh_tens
     if (head_dim == 64) {
         st = flash(s, q->ptr, k->ptr, v->ptr, t->ptr, heads, tokens, heads, false);
     } else {
-        const float scale = 1.0f / sqrtf((float)head_dim);
-        st = launch(s, "attention_online", [&] {
-            return vh::launch_attention_online(s.stream, q->ptr, k->ptr, v->ptr, t->ptr, heads,
-                                               tokens, head_dim, scale);
-        });
+        // Rows zero-padded to 64 dims run through the flash kernel with the
+        // 1/sqrt(head_dim) scale; the output keeps the first head_dim columns.
+        const size_t padded = ht * 64;
+        float *pad = nullptr;
+        st = dalloc(s, 4 * padded, &pad, "attention padding allocation");
+        if (!st) {
+            float *pq = pad, *pk = pad + padded, *pv = pad + 2 * padded, *po = pad + 3 * padded;
+            st = launch(s, "attention_pad", [&] {
+                return vh::launch_pad_rows64(s.stream, q->ptr, k->ptr, v->ptr, pq, pk, pv, ht,
+                                             head_dim);
+            });
+            if (!st)
+                st = flash(s, pq, pk, pv, po, heads, tokens, heads, false, nullptr, nullptr,
+                           nullptr, 1.0f / sqrtf((float)head_dim));
+            if (!st)
+                st = launch(s, "attention_unpad", [&] {
+                    return vh::launch_unpad_rows(s.stream, po, t->ptr, ht, head_dim);
+                });
+            hipFreeAsync(pad, s.stream);
+        }
     }
     if (st) {
         delete t;
@@ -993,7 +1017,7 @@ extern "C" vh_status vh_flash_attention_f32_da3_base(const vh_runtime *rt, const
     if (mul_overflows(heads, tokens, &ht) || mul_overflows(ht, 64, &expected) ||
         q->len != expected || k->len != expected || v->len != expected)
         return mismatch(q->len, expected, "vh_flash_attention_f32_da3_base");
-    if (tokens > INT32_MAX || heads > 65535)
+    if (tokens > INT32_MAX || heads > 65535 || !flash_grid_fits(heads, tokens))
         return fail(VH_ERR_KERNEL, "flash attention shape exceeds the launch grid");
     GUARD_BEGIN
     RtState &s = *rt->s;
