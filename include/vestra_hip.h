@@ -137,6 +137,21 @@ vh_status vh_attention_online_f32(const vh_runtime *rt, const vh_tensor *q, cons
 vh_status vh_flash_attention_f32_da3_base(const vh_runtime *rt, const vh_tensor *q,
                                           const vh_tensor *k, const vh_tensor *v, size_t heads,
                                           size_t tokens, int token_major, vh_tensor **out);
+/* No counterpart in the reference.  vh_flash_attention_f32_da3_base for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): it calls no
+ * allocator.  The caller passes `out` (heads*tokens*64 floats, layout as
+ * above).  The key-split partials live in a 64 MiB device array of the
+ * library, one per GPU, reserved until the process ends; heads*tokens above
+ * 63550 is rejected with VH_ERR_KERNEL before any launch.  Every call on a
+ * GPU shares that GPU's array: calls ordered on one stream are safe, calls
+ * that overlap on one GPU (runtimes on different streams, host threads
+ * without ordering) race.  Results are bit-identical to the allocating entry
+ * point's. */
+vh_status vh_flash_attention_f32_da3_base_into(const vh_runtime *rt, const vh_tensor *q,
+                                               const vh_tensor *k, const vh_tensor *v,
+                                               size_t heads, size_t tokens, int token_major,
+                                               vh_tensor *out);
 
 /* ---- layout (src/cuda.rs:927-1175) ---------------------------------------- */
 vh_status vh_split_qkv_hnd_f32(const vh_runtime *rt, const vh_tensor *qkv, size_t tokens,

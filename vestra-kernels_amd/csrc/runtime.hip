@@ -91,6 +91,7 @@ struct RtState {
     size_t aq_bytes = 0;
     float *tw = nullptr;                        // balanced-tail GEMM partials
     unsigned *tcnt = nullptr;                   // and arrival counters (zeroed once)
+    float *scratch = nullptr;                   // this device's copy of `scratch` (below)
 
     bool profile = false;
     std::vector<ProfileRec> pending;
@@ -588,6 +589,43 @@ vh_status prepare_q8_from_f32(RtState &s, size_t K, size_t N, const float *w, co
 }  // namespace
 
 // =============================================================================
+// no-allocation scratch
+// =============================================================================
+
+// Key-split partials of vh_flash_attention_f32_da3_base_into: a file-scope
+// device array, one copy per GPU, held until the process ends.  Host code
+// never passes `scratch` itself (on the host the name is only a stand-in);
+// it passes the device address hipGetSymbolAddress returned for the current
+// device, cached per device by scratch_init.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+constexpr size_t kScratchFloats = kScratchBytes / sizeof(float);
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[kMaxScratchDevices] = {};
+
+// With `device` current: its address of `scratch`, looked up once.
+vh_status scratch_init(int device, float **out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0 || device >= kMaxScratchDevices)
+        return fail(VH_ERR_INITIALIZE, "no scratch slot for HIP device " + std::to_string(device));
+    if (!g_scratch_ptr[device]) {
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(VH_ERR_INITIALIZE, hip_msg("scratch symbol address", e));
+        g_scratch_ptr[device] = static_cast<float *>(p);
+    }
+    *out = g_scratch_ptr[device];
+    return VH_OK;
+}
+
+}  // namespace
+
+// =============================================================================
 // errors
 // =============================================================================
 
@@ -620,6 +658,7 @@ extern "C" vh_status vh_runtime_new(size_t device, vh_runtime **out) {
     if (e != hipSuccess)
         return fail(VH_ERR_INITIALIZE, "failed to initialize HIP device " + std::to_string(device) +
                                            ": " + hipGetErrorString(e));
+    TRY(scratch_init(s->device, &s->scratch));
     // Keep freed blocks in the stream-ordered pool instead of returning them
     // to the driver at every synchronisation.
     hipMemPool_t pool = nullptr;
@@ -1030,6 +1069,44 @@ extern "C" vh_status vh_flash_attention_f32_da3_base(const vh_runtime *rt, const
         return st;
     }
     *out = t;
+    return VH_OK;
+    GUARD_END
+}
+
+extern "C" vh_status vh_flash_attention_f32_da3_base_into(const vh_runtime *rt,
+                                                          const vh_tensor *q, const vh_tensor *k,
+                                                          const vh_tensor *v, size_t heads,
+                                                          size_t tokens, int token_major,
+                                                          vh_tensor *out) {
+    const char *what = "vh_flash_attention_f32_da3_base_into";
+    NEED(rt, what);
+    NEED(q, what);
+    NEED(k, what);
+    NEED(v, what);
+    NEED(out, what);
+    size_t ht = 0, expected = 0;
+    if (mul_overflows(heads, tokens, &ht) || mul_overflows(ht, 64, &expected) ||
+        q->len != expected || k->len != expected || v->len != expected)
+        return mismatch(q->len, expected, what);
+    if (out->len != expected) return mismatch(out->len, expected, what);
+    if (tokens > INT32_MAX || heads > 65535 || !flash_grid_fits(heads, tokens))
+        return fail(VH_ERR_KERNEL, "flash attention shape exceeds the launch grid");
+    // Room for the partials of the largest key split the launcher may pick,
+    // so that it picks the split the allocating entry point picks.
+    const size_t max_rows = kScratchFloats / vh::flash_workspace_floats(1, 1);
+    if (ht > max_rows)
+        return fail(VH_ERR_KERNEL, std::string(what) + ": heads*tokens = " + std::to_string(ht) +
+                                       " exceeds the no-allocation limit of " +
+                                       std::to_string(max_rows) + " (64 MiB of key-split partials)");
+    if (heads * tokens == 0) return VH_OK;
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    if (!s.scratch) return fail(VH_ERR_INITIALIZE, std::string(what) + ": no scratch on this device");
+    hipError_t e = vh::launch_flash_attention(s.stream, q->ptr, k->ptr, v->ptr, out->ptr, heads,
+                                              tokens, heads, token_major != 0, s.scratch,
+                                              kScratchFloats);
+    if (e != hipSuccess) return fail(VH_ERR_KERNEL, hip_msg(what, e));
     return VH_OK;
     GUARD_END
 }

@@ -105,6 +105,7 @@ SIGNATURES = [
     ("vh_layernorm_f32_cpu_order", _S, [_p, _p, _p, _p, _sz, _sz, ctypes.c_float, _pp]),
     ("vh_attention_online_f32", _S, [_p, _p, _p, _p, _sz, _sz, _sz, _pp]),
     ("vh_flash_attention_f32_da3_base", _S, [_p, _p, _p, _p, _sz, _sz, ctypes.c_int, _pp]),
+    ("vh_flash_attention_f32_da3_base_into", _S, [_p, _p, _p, _p, _sz, _sz, ctypes.c_int, _p]),
     ("vh_split_qkv_hnd_f32", _S, [_p, _p, _sz, _sz, _sz, _pp, _pp, _pp]),
     ("vh_hnd_to_token_f32", _S, [_p, _p, _sz, _sz, _sz, _pp]),
     ("vh_token_to_chw_f32", _S, [_p, _p, _sz, _sz, _pp]),
@@ -535,6 +536,14 @@ class Runtime:
     def flash_attention_f32_da3_base(self, q, k, v, heads, tokens, token_major=False) -> Tensor:
         return self._out(lib().vh_flash_attention_f32_da3_base, q.handle, k.handle, v.handle,
                          heads, tokens, 1 if token_major else 0)
+
+    def flash_attention_f32_da3_base_into(self, q, k, v, heads, tokens, token_major,
+                                          out: Tensor) -> None:
+        """The same attention into a caller-provided `out`, with no device
+        allocation (key-split partials in the library's per-GPU scratch)."""
+        _check(lib().vh_flash_attention_f32_da3_base_into(
+            self._h, q.handle, k.handle, v.handle, heads, tokens, 1 if token_major else 0,
+            out.handle))
 
     # -- layout
     def split_qkv_hnd_f32(self, qkv, tokens, heads, head_dim):
