@@ -35,6 +35,30 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == bound, (set(names) ^ bound)
 
 
+RUST_BINDING = ROOT / "vestra-kernels_amd" / "rust" / "hip.rs"
+# Not bound in Rust: clones share one runtime through Arc, and is_empty uses len.
+RUST_UNBOUND = {"vh_runtime_clone", "vh_tensor_is_empty"}
+
+
+def test_rust_binding_declares_the_header():
+    """The `hip` feature's FFI block (rust/hip.rs) declares every C-ABI
+    function with the header's parameter count (it is compiled by the
+    crate's build, not here)."""
+    text = RUST_BINDING.read_text()
+    block = text[text.index('unsafe extern "C" {'):]
+    block = block[:block.index("\n}\n")]
+    rust = dict(re.findall(r"fn (vh_[a-z0-9_]+)\(([^)]*)\)", block, flags=re.S))
+    names = set(declared_functions())
+    assert set(rust) == names - RUST_UNBOUND, set(rust) ^ (names - RUST_UNBOUND)
+    header = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for name, params in rust.items():
+        c_params = re.search(name + r"\s*\(([^)]*)\)", header).group(1)
+        n_c = 0 if c_params.strip() in ("", "void") else c_params.count(",") + 1
+        n_r = 0 if not params.strip() else params.count(",") + 1
+        assert n_c == n_r, (name, n_c, n_r)
+    assert 'compile_error!("features `cuda` and `hip` are exclusive' in text
+
+
 def test_null_handles_fail_before_any_device_call():
     L = vh.lib()
     out = ctypes.c_void_p()
