@@ -411,14 +411,24 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     if constexpr (TAIL) {
         if (piece >= 0) {
             // Publish this piece's partial (coalesced: consecutive threads,
-            // consecutive floats), then count it in.  Partials are written
-            // and read with device-scope accesses, which bypass the caches
-            // that are not coherent across XCDs, so no cache-wide writeback
-            // or invalidate is needed (an agent-scope fence here costs both,
-            // and doubled the kernel's time).  Every thread waits for its
-            // stores to complete before the barrier, the counter is bumped
-            // after it, and the last piece reads the partials only after
-            // seeing the count.  No piece waits for another, so the grid
+            // consecutive floats), then count it in.  Ordering, step by step:
+            //  1. Partials are agent-scope atomic stores, which write through
+            //     the XCD's L2 (not coherent across XCDs) to the point where
+            //     every XCD reads; none stays dirty in L2.
+            //  2. Each thread then waits for its stores to be acknowledged
+            //     (vmcnt(0) counts stores on gfx9).  The wait is inline asm
+            //     with a memory clobber, so the compiler cannot move a store
+            //     past it.
+            //  3. The barrier orders every thread's wait before thread 0's
+            //     agent-scope counter increment.
+            //  4. The piece that sees the last count reads the partials with
+            //     agent-scope atomic loads, after the barrier that follows
+            //     the increment's return.  Those loads bypass the L2, so they
+            //     cannot hit stale lines.
+            // This is what an agent-scope release / acquire pair would
+            // provide, minus its L2-wide writeback and invalidate, which
+            // only non-atomic data needs.  An agent-scope fence here doubled
+            // the kernel's time.  No piece waits for another, so the grid
             // drains whatever the residency.
             __shared__ int tail_last;
             constexpr int PER = FM * FN * 4;
@@ -432,7 +442,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                     for (int r = 0; r < 4; r++)
                         __hip_atomic_store(mine + ((i * FN + j) * 4 + r) * NT + tid, acc[i][j][r],
                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_s_waitcnt(0);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             if (tid == 0)
                 tail_last = __hip_atomic_fetch_add(ep.tail_cnt + tail_u, 1u, __ATOMIC_RELAXED,
