@@ -50,6 +50,7 @@ def _declare(L):
     sig("vko_force_scalar", None, ctypes.c_int)
     sig("vko_f16_sweep", ctypes.c_uint64, ctypes.c_uint32)
     sig("vko_get_threads", ctypes.c_int)
+    sig("vko_rust_max", ctypes.c_float, ctypes.c_float, ctypes.c_float)
     sig("vko_f32_to_f16", ctypes.c_uint16, ctypes.c_float)
     sig("vko_f16_to_f32", ctypes.c_float, ctypes.c_uint16)
     sig("vko_f32_to_f16_hw", ctypes.c_uint16, ctypes.c_float)
@@ -134,6 +135,11 @@ def force_scalar(on: bool) -> None:
 def f16_sweep(step: int = 1) -> int:
     """Mismatches of the software f16 conversions against F16C."""
     return int(lib().vko_f16_sweep(step))
+
+
+def rust_max(a: float, b: float) -> float:
+    """f32::max as the oracle restates it (any NaN operand is ignored)."""
+    return float(lib().vko_rust_max(ctypes.c_float(a), ctypes.c_float(b)))
 
 
 def set_threads(n: int) -> None:

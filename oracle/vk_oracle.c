@@ -55,8 +55,17 @@ int vko_get_threads(void) { return g_threads > 0 ? g_threads : omp_get_max_threa
 /* Rust's `iter().sum::<f32>()` folds from -0.0 (core::iter::Sum for f32). */
 #define RUST_SUM_INIT (-0.0f)
 
-/* Rust f32::max / f32::min: IEEE maxNum/minNum (a NaN operand is ignored). */
-static inline float rmax(float a, float b) { return fmaxf(a, b); }
+/* Rust f32::max (core f32::max): the larger operand, and "if one of the
+ * arguments is NaN, then the other argument is returned" -- every NaN,
+ * signalling ones included (IEEE maxNum would quiet a signalling NaN, and
+ * glibc fmaxf does). */
+static inline float rmax(float a, float b) {
+    if (isnan(b)) return a;
+    if (isnan(a)) return b;
+    return fmaxf(a, b);
+}
+
+float vko_rust_max(float a, float b) { return rmax(a, b); }
 
 /* ------------------------------------------------------------------------ */
 /* f16: half 2.7.1 f16::from_f32 / to_f32 (IEEE binary16, RNE)              */

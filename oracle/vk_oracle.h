@@ -35,6 +35,8 @@ int vko_has_avx512(void);        /* avx512f+bw+vnni+fma, src/dispatch.rs:34-48 *
 void vko_set_threads(int n);     /* <=0 restores the default (all cores) */
 void vko_force_scalar(int on);   /* 1: take the reference's non-AVX-512 paths */
 int vko_get_threads(void);
+/* Rust f32::max: the other operand when one is NaN (any NaN). */
+float vko_rust_max(float a, float b);
 
 /* ---- f16 (half 2.7.1 from_f32/to_f32: IEEE round-to-nearest-even) ------ */
 uint16_t vko_f32_to_f16(float x);

@@ -102,3 +102,24 @@ def test_gemm_q8_0_matches_float64_block_sum():
     isum = np.einsum("ibl,jbl->ijb", qa, qb)
     ref = np.einsum("ib,jb,ijb->ij", da, db, isum.astype(np.float64))
     assert np.abs(c.reshape(m, n) - ref).max() <= 1e-6 * np.abs(ref).max()
+
+
+def test_quantize_block_max_ignores_every_nan():
+    """quantize_row_q8_0 folds amax from 0 with f32::max (src/q8_0_dot.rs:35),
+    which returns the other operand when one is NaN and, unlike IEEE maxNum,
+    treats signalling NaNs like quiet ones (core f32::max).  So a block of
+    NaNs has amax 0 (d = 0, every value 0) and a NaN never hides the other
+    values' maximum, wherever it sits in the block."""
+    snan, qnan = np.uint32(0x7F800005), np.uint32(0x7FC00000)
+    assert O.rust_max(1.0, float("nan")) == 1.0 and O.rust_max(float("nan"), 2.0) == 2.0
+    for nan in (snan, qnan):
+        block = np.full(32, nan, np.uint32).view(np.float32)
+        b = O.quantize_rows_q8_0(block, 1, 32)
+        assert b["d"][0] == 0 and not b["qs"].any()
+        for pos in (0, 17, 31):
+            bits = np.full(32, np.float32(1.0).view(np.uint32), np.uint32)
+            bits[pos] = nan
+            b = O.quantize_rows_q8_0(bits.view(np.float32), 1, 32)
+            assert b["d"][0] == O.f32_to_f16(np.float32(1.0) / np.float32(127.0))
+            q = b["qs"][0]
+            assert q[pos] == 0 and (np.delete(q, pos) == 127).all()
