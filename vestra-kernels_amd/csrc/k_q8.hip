@@ -14,6 +14,7 @@
 // three separately rounded ops.  (Holding the int8 values as halves for the
 // f16 MFMA would drop the conversion, but doubles the operand bytes and
 // measured slower: the operands no longer stay in L2.)
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -27,49 +28,93 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
-// quantize_row_q8_0 (src/q8_0_dot.rs:27-46): four lanes per 32-value block,
-// eight values each; amax is a max (order-free) over the four lanes, taken
-// with two DPP quad permutations (lane ^ 1, lane ^ 2).  Lane groups walk the
-// block-major output slots in order (slot j * rows + r holds row r's k-slice
-// j), so a wave writes 512 contiguous bytes of values and 32 of scales and
-// reads sixteen 128-byte row segments.  A 2-D grid (x: rows, y: k-slices)
-// keeps the slot arithmetic free of 64-bit division.
-__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x,
-                                                            int8_t *__restrict__ qs,
-                                                            uint16_t *__restrict__ dbits,
-                                                            int rows, int nbr) {
-    // blockIdx.y is the k-slice j; the threads of x walk its rows.
-    const int j = blockIdx.y;
-    const int r0 = (blockIdx.x * blockDim.x + threadIdx.x) >> 2;
-    const int part = threadIdx.x & 3;
-    const bool live = r0 < rows;
-    const int r = live ? r0 : rows - 1;  // idle lanes shadow the last row
-    const size_t dst = (size_t)j * rows + r;  // block-major slot
-    const size_t bb = (size_t)r * nbr + j;    // row-major block
-    const f32x4 *src = reinterpret_cast<const f32x4 *>(x + bb * 32) + 2 * part;
-    const f32x4 v0 = src[0], v1 = src[1];
-    float amax = fmaxf(fmaxf(fmaxf(fabsf(v0[0]), fabsf(v0[1])), fmaxf(fabsf(v0[2]), fabsf(v0[3]))),
-                       fmaxf(fmaxf(fabsf(v1[0]), fabsf(v1[1])), fmaxf(fabsf(v1[2]), fabsf(v1[3]))));
-    amax = fmaxf(amax, dpp_f32<0xb1>(amax));
-    amax = fmaxf(amax, dpp_f32<0x4e>(amax));
-    const float d = div_rn(amax, 127.0f);
-    const float inv = d != 0.0f ? div_rn(1.0f, d) : 0.0f;
-    if (!live) return;
-    if (part == 0) dbits[dst] = __builtin_bit_cast(uint16_t, (_Float16)d);
-    uint32_t w[2] = {0, 0};
+// quantize_row_q8_0 (src/q8_0_dot.rs:27-46) of a tile of R consecutive rows
+// per workgroup (8, or 4 when there are few rows), up to 768 columns (24
+// blocks) at a time:
+//  - loads: float4 u of the tile is row u / (cw/4), column 4 (u % (cw/4)),
+//    so each load instruction of the workgroup reads 4 KB of consecutive row
+//    memory (the rows are adjacent in memory when cw == k) and a block's
+//    eight float4 sit in eight adjacent lanes;
+//  - arithmetic: amax over the block's lanes (three DPP steps: lane ^ 1,
+//    lane ^ 2, then the mirror pairing the two quads), d = amax / 127 and
+//    1 / d correctly rounded, d stored as binary16 (RNE), each value
+//    roundf(x * (1/d)) clamped to +-127 (NaN -> 0);
+//  - stores: through LDS, so that block j of the R rows, block-major slots
+//    j * rows + r0 .. r0 + R - 1, is written as one run of 32 R bytes.
+// NT: non-temporal loads.  k % 32 == 0; x 16-byte aligned (device tensors
+// and workspaces always are).
+template <bool NT, int R>
+__global__ __launch_bounds__(256) void quantize_tile_q8_0_kernel(const float *__restrict__ x,
+                                                                 int8_t *__restrict__ qs,
+                                                                 uint16_t *__restrict__ dbits,
+                                                                 int rows, int nbr) {
+    constexpr int CB = 24;  // blocks per column chunk
+    static_assert(R * CB * 8 % 256 == 0, "whole float4 per thread");
+    __shared__ __attribute__((aligned(16))) uint32_t sq[CB][R][8];
+    __shared__ uint16_t sd[CB][R];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int r0 = blockIdx.x * R;
+    const int nr = min(R, rows - r0);
+    for (int j0 = 0; j0 < nbr; j0 += CB) {
+        const int cb = min(CB, nbr - j0);  // blocks in this chunk
+        const int c4 = cb * 8;             // float4 per row in this chunk
+        constexpr int U = R * CB * 8 / 256;  // float4 per thread
+        f32x4 v[U];
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        float q = roundf(mul_rn(e < 4 ? v0[e] : v1[e - 4], inv));  // f32::round: half away from zero
-        int qi;
-        if (isnan(q)) {
-            qi = 0;  // `NaN as i8` saturates to 0
-        } else {
-            q = fminf(fmaxf(q, -127.0f), 127.0f);
-            qi = (int)q;
+        for (int i = 0; i < U; i++) {
+            const int u = i * 256 + tid;
+            const int r = min(u / c4, nr - 1), c = u % c4;  // past the tile: a clamped row
+            const f32x4 *src = reinterpret_cast<const f32x4 *>(x + (size_t)(r0 + r) * nbr * 32 +
+                                                               (size_t)j0 * 32) + c;
+            if constexpr (NT) v[i] = __builtin_nontemporal_load(src);
+            else v[i] = *src;
         }
-        w[e >> 2] |= ((uint32_t)(qi & 0xff)) << (8 * (e & 3));
+#pragma unroll
+        for (int i = 0; i < U; i++) {
+            const int u = i * 256 + tid;
+            float amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) amax = q8_absmax(amax, v[i][e]);
+            amax = q8_absmax(amax, dpp_f32<0xb1>(amax));
+            amax = q8_absmax(amax, dpp_f32<0x4e>(amax));
+            amax = q8_absmax(amax, dpp_f32<0x141>(amax));
+            float d, inv;
+            q8_scale(amax, d, inv);
+            uint32_t w = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float q = roundf(mul_rn(v[i][e], inv));  // f32::round: half away from zero
+                int qi;
+                if (isnan(q)) {
+                    qi = 0;  // `NaN as i8` saturates to 0
+                } else {
+                    q = fminf(fmaxf(q, -127.0f), 127.0f);
+                    qi = (int)q;
+                }
+                w |= ((uint32_t)(qi & 0xff)) << (8 * e);
+            }
+            const int r = u / c4, c = u % c4, jb = c >> 3;
+            if (r < nr) {
+                sq[jb][r][c & 7] = w;
+                if ((lane & 7) == 0) sd[jb][r] = __builtin_bit_cast(uint16_t, (_Float16)d);
+            }
+        }
+        __syncthreads();
+        // Block column jb: R slots x 32 bytes = 2R chunks of 16 bytes.
+        for (int u = tid; u < cb * 2 * R; u += 256) {
+            const int jb = u / (2 * R), r = (u % (2 * R)) >> 1, half = u & 1;
+            if (r < nr) {
+                const size_t slot = (size_t)(j0 + jb) * rows + r0 + r;
+                reinterpret_cast<uint4 *>(qs + slot * 32)[half] =
+                    reinterpret_cast<const uint4 *>(&sq[jb][r][0])[half];
+            }
+        }
+        for (int u = tid; u < cb * R; u += 256) {
+            const int jb = u / R, r = u % R;
+            if (r < nr) dbits[(size_t)(j0 + jb) * rows + r0 + r] = sd[jb][r];
+        }
+        __syncthreads();
     }
-    reinterpret_cast<uint2 *>(qs + dst * 32)[part] = make_uint2(w[0], w[1]);
 }
 
 // LayerNorm of a row (the arithmetic of layernorm_kernel: ln_row_stats and
@@ -104,12 +149,14 @@ __global__ __launch_bounds__(256) void layernorm_q8_0_kernel(const float *__rest
         const int gi = min(idx, n4 - 1);
         const f32x4 y = ln_apply(r[j], mean, inv, reinterpret_cast<const f32x4 *>(gamma)[gi],
                                  reinterpret_cast<const f32x4 *>(beta)[gi]);
-        float amax = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
-        amax = fmaxf(amax, dpp_f32<0xb1>(amax));
-        amax = fmaxf(amax, dpp_f32<0x4e>(amax));
-        amax = fmaxf(amax, dpp_f32<0x141>(amax));
-        const float d = div_rn(amax, 127.0f);
-        const float qinv = d != 0.0f ? div_rn(1.0f, d) : 0.0f;
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) amax = q8_absmax(amax, y[e]);
+        amax = q8_absmax(amax, dpp_f32<0xb1>(amax));
+        amax = q8_absmax(amax, dpp_f32<0x4e>(amax));
+        amax = q8_absmax(amax, dpp_f32<0x141>(amax));
+        float d, qinv;
+        q8_scale(amax, d, qinv);
         uint32_t w = 0;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
@@ -173,7 +220,10 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
                                                         int K, Q8Epi ep) {
     static_assert(EPI != Epi::Qkv || FN == 2, "the QKV epilogue pairs fragments j = 0, 1");
     constexpr int TR = 32 * FM, TC = 32 * FN;  // workgroup tile
-    constexpr int QPF = 4;  // prefetch distance in blocks
+    // Prefetch distance in blocks: 4 for the larger tiles; the 32x32 tile
+    // (16x16 per wave) measured 7-10% faster with 2 (fewer registers held).
+    constexpr int QPF = FM * FN == 1 ? 2 : 4;
+    static_assert(QCH % QPF == 0, "scale chunks hold whole prefetch groups");
     __shared__ __attribute__((aligned(16))) float sa[QCH][TR];
     __shared__ __attribute__((aligned(16))) float sb[QCH][TC];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -340,13 +390,13 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
                         if (ep.bias) v = add_rn(v, bias[j]);
                         g[j] = idx < ep.tail_start ? gelu_avx512_form(v) : gelu_scalar_form(v);
                     }
-                    float amax = fmaxf(fabsf(g[0]), fabsf(g[1]));
-                    amax = fmaxf(amax, dpp_f32<0xb1>(amax));
-                    amax = fmaxf(amax, dpp_f32<0x4e>(amax));
-                    amax = fmaxf(amax, dpp_f32<0x141>(amax));
-                    amax = fmaxf(amax, dpp_f32<0x140>(amax));
-                    const float d = div_rn(amax, 127.0f);
-                    const float qinv = d != 0.0f ? div_rn(1.0f, d) : 0.0f;
+                    float amax = q8_absmax(q8_absmax(0.0f, g[0]), g[1]);
+                    amax = q8_absmax(amax, dpp_f32<0xb1>(amax));
+                    amax = q8_absmax(amax, dpp_f32<0x4e>(amax));
+                    amax = q8_absmax(amax, dpp_f32<0x141>(amax));
+                    amax = q8_absmax(amax, dpp_f32<0x140>(amax));
+                    float d, qinv;
+                    q8_scale(amax, d, qinv);
                     if (row >= M) continue;
                     const size_t slot = kslice * M + row;
 #pragma unroll
@@ -440,9 +490,21 @@ hipError_t launch_quantize_q8_0(hipStream_t s, const float *x, int8_t *qs, uint1
                                 size_t rows, size_t k) {
     size_t nblocks = rows * (k / 32);
     if (nblocks == 0) return hipSuccess;
-    if (rows > (size_t)INT32_MAX / 4 || k / 32 > 65535) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((rows * 4 + 255) / 256), (unsigned)(k / 32));
-    quantize_q8_0_kernel<<<grid, 256, 0, s>>>(x, qs, d, (int)rows, (int)(k / 32));
+    if (rows > (size_t)INT32_MAX / 4 || k / 32 > (size_t)INT32_MAX / rows) return hipErrorInvalidValue;
+    // Eight rows per workgroup (measured faster than sixteen past the
+    // Infinity Cache), four below 2048 rows so that small inputs still spread
+    // over every CU.  Past 128 MiB of input the loads are non-temporal:
+    // nothing of it stays cached for a consumer at that size.
+    const int nbr = (int)(k / 32);
+    const bool nt = rows * k * 4 >= (size_t(128) << 20);
+    if (rows >= 2048) {
+        const unsigned blocks = (unsigned)((rows + 7) / 8);
+        if (nt) quantize_tile_q8_0_kernel<true, 8><<<blocks, 256, 0, s>>>(x, qs, d, (int)rows, nbr);
+        else quantize_tile_q8_0_kernel<false, 8><<<blocks, 256, 0, s>>>(x, qs, d, (int)rows, nbr);
+    } else {
+        const unsigned blocks = (unsigned)((rows + 3) / 4);
+        quantize_tile_q8_0_kernel<false, 4><<<blocks, 256, 0, s>>>(x, qs, d, (int)rows, nbr);
+    }
     return hipGetLastError();
 }
 

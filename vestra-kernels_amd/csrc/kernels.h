@@ -42,6 +42,10 @@ hipError_t launch_rope_table_device(hipStream_t s, const float *pos, size_t toke
                                     float *rot);
 hipError_t launch_transpose(hipStream_t s, const float *in, float *out, size_t rows,
                             size_t cols);
+// Streaming copy of n floats (non-temporal, four float4 per thread in
+// flight) for 16-byte-aligned, non-overlapping runs of at least 128 MiB.
+bool stream_copy_applies(float *dst, const float *src, size_t n);
+hipError_t launch_stream_copy(hipStream_t s, float *dst, const float *src, size_t n);
 
 // ---- attention (k_attention.hip) ----------------------------------------
 // Head dims below 64 through the flash kernel: q/k/v rows of hd floats

@@ -760,9 +760,13 @@ extern "C" float *vh_tensor_device_ptr(const vh_tensor *tensor) {
 // copies / residual
 // =============================================================================
 
+// Device copies: the streaming copy kernel for large 16-byte-aligned runs
+// (non-temporal, faster than the runtime's copy engine path), else
+// hipMemcpyAsync.
 static vh_status d2d(RtState &s, float *dst, const float *src, size_t n, const char *what) {
     if (n == 0) return VH_OK;
     return launch(s, what, [&] {
+        if (vh::stream_copy_applies(dst, src, n)) return vh::launch_stream_copy(s.stream, dst, src, n);
         return hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyDeviceToDevice, s.stream);
     });
 }
