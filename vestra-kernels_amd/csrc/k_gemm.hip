@@ -449,19 +449,36 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                                                    __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(ep.tail_splits - 1);
             __syncthreads();
             if (!tail_last) return;
-            // The sum in piece order, whichever piece finished last.
-            float *parts = ep.partial + tile_base;
+            // The sum in piece order, whichever piece finished last.  Every
+            // piece's values are loaded before the first add (a uniform
+            // branch per piece, no loop-carried wait), so the loads are in
+            // flight together rather than one round trip per piece and value.
+            constexpr int MAXS = 4;  // tail_splits <= 4 (tail_plan)
+            const float *parts = ep.partial + tile_base;
+            float pv[MAXS][PER];
+#pragma unroll
+            for (int p = 0; p < MAXS; p++) {
+                if (p < ep.tail_splits) {
+#pragma unroll
+                    for (int e = 0; e < PER; e++)
+                        pv[p][e] = __hip_atomic_load(parts + (size_t)(p * PER + e) * NT + tid, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < PER; e++) pv[p][e] = 0.0f;
+                }
+            }
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int j = 0; j < FN; j++)
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        const size_t o = (size_t)((i * FN + j) * 4 + r) * NT + tid;
-                        float v = __hip_atomic_load(parts + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        for (int p = 1; p < ep.tail_splits; p++)
-                            v = v + __hip_atomic_load(parts + (size_t)p * PER * NT + o, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
+                        const int e = (i * FN + j) * 4 + r;
+                        float v = pv[0][e];
+#pragma unroll
+                        for (int p = 1; p < MAXS; p++)
+                            if (p < ep.tail_splits) v = v + pv[p][e];
                         acc[i][j][r] = v;
                     }
             if (tid == 0) __hip_atomic_store(ep.tail_cnt + tail_u, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -917,15 +934,14 @@ bool tail_plan(const GemmArgs &g, const Tile &t, TailPlan *plan) {
     const long count8 = (rem + 7) / 8 * 8;
     if (full == 0 || rem == 0 || full % 8 != 0) return false;
     const long ktiles = (long)(g.k / 32);
-    // Measured on MI355X (fc1-shaped, N = 3072, K = 768): 2 pieces of the
-    // 128-tile tail at M = 512 and of the 112-tile tail at M = 832 cut the
-    // launch by 9% and 12% (predicted loads -25% and -17%), while 3 pieces at
-    // M = 865 (-11% predicted) made it 5% slower and 3 pieces at M = 3460
-    // (-6%) changed nothing: the pieces' partial traffic and fix-up cost about
-    // a tenth of a round.  Hence a tail only for a predicted cut of 15% or
-    // more, unless forced.
+    // Measured on MI355X (fc1-shaped, N = 3072, K = 768, per-launch events,
+    // tail off -> on): M = 512 38.5 -> 32.6 us, 832 51.8 -> 46.1, 865 52.4 ->
+    // 50.1, 1730 98.7 -> 91.8, 3460 175.9 -> 171.8 (predicted loads -25%,
+    // -17%, -11%, -12%, -6%).  The fix-up's partial reads are all in flight
+    // at once; when each waited for the one before, the tail lost at M = 865
+    // and 3460.  Hence a tail for any predicted cut of 5% or more.
     const double whole = (double)(full / cus + 1);
-    double best = forced ? whole : whole * 0.85;
+    double best = forced ? whole : whole * 0.95;
     int pick = 0;
     for (int sp = 2; sp <= 4; sp++) {
         if (ktiles % sp != 0 || ktiles / sp < 4) continue;
