@@ -296,8 +296,11 @@ def gpu_elementwise(reps: int = 20) -> dict:
         return (f"add {n}", lambda: rt.add_f32_in_place(a1, a2), 3 * n * 4, "add")
 
     def q8_case(rows):
+        # Into one preallocated Q8_0 tensor (quantize_row_q8_0(x, out)): an
+        # allocating call per launch makes the burst host-bound at this size.
         x = rt.upload_f32(big(33, rows * D))
-        return (f"quantize_q8_0 {rows}x{D}", lambda: rt.quantize_q8_0(x, rows, D),
+        out = rt.quantize_q8_0(x, rows, D)
+        return (f"quantize_q8_0 {rows}x{D}", lambda: rt.quantize_q8_0_into(x, rows, D, out),
                 rows * D * 4 + rows * D + rows * D // 16, "quantize_q8_0")
 
     def rope_case(heads, grid_h, grid_w):

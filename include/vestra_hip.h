@@ -229,6 +229,12 @@ size_t vh_q8_tensor_k(const vh_q8_tensor *tensor);
  * [rows, k] f32 tensor, k % 32 == 0.  Bit-exact. */
 vh_status vh_quantize_q8_0(const vh_runtime *rt, const vh_tensor *x, size_t rows, size_t k,
                            vh_q8_tensor **out);
+/* quantize_row_q8_0(x, out) (src/q8_0_dot.rs:27-46) into an existing
+ * [rows, k] Q8_0 tensor, as the reference writes a caller's block slice:
+ * VH_ERR_LENGTH_MISMATCH ("x.len() must be out.len()*QK8_0", the reference's
+ * assert) unless out holds rows x k / 32 blocks and x rows * k floats. */
+vh_status vh_quantize_q8_0_into(const vh_runtime *rt, const vh_tensor *x, size_t rows, size_t k,
+                                vh_q8_tensor *out);
 /* Kernels::gemm_q8_0 (src/dispatch.rs:91-105, oracle src/scalar.rs:25-56):
  * C[m,n] = sum_b (d_a*d_b)*isum_b with a_q [m,k] and b_q [n,k]; int8 MFMA
  * block sums, f32 combine in block order.  Bit-exact. */

@@ -428,7 +428,9 @@ def test_qk_norm_rope_production_shape(rt):
 
 # ---- Q8_0 (bit-exact) -------------------------------------------------------------
 
-@pytest.mark.parametrize("rows,k", [(865, 768), (3, 32), (8, 64)])
+# 4096 and 2048 rows take the 8-row tiles with one 16-byte store per block
+# column of scales; 4100 rows end on a partial tile (2-byte scale stores).
+@pytest.mark.parametrize("rows,k", [(865, 768), (3, 32), (8, 64), (4096, 768), (4100, 768), (2048, 96)])
 def test_quantize_q8_0_bit_exact(rt, rows, k):
     x = seeded.normal(81 + rows, rows * k)
     x[:32] = 0.0  # an all-zero block: d = 0, inv = 0
@@ -437,6 +439,28 @@ def test_quantize_q8_0_bit_exact(rt, rows, k):
     got = rt.q8_0_download(rt.quantize_q8_0(rt.upload_f32(x), rows, k))
     assert np.array_equal(got["d"], exp["d"])
     assert np.array_equal(got["qs"], exp["qs"])
+
+
+def test_quantize_into_an_existing_tensor(rt):
+    """quantize_row_q8_0(x, out) writes the caller's blocks: equal to the
+    allocating entry point and to the oracle, twice into the same tensor (the
+    second call overwrites every block); a tensor of another shape is the
+    reference's length assert."""
+    rows, k = 4096, 768
+    out = rt.quantize_q8_0(rt.upload_f32(np.ones(rows * k, np.float32)), rows, k)
+    for seed in (4701, 4702):
+        x = seeded.normal(seed, rows * k)
+        xt = rt.upload_f32(x)
+        rt.quantize_q8_0_into(xt, rows, k, out)
+        got = rt.q8_0_download(out)
+        assert np.array_equal(got, rt.q8_0_download(rt.quantize_q8_0(xt, rows, k)))
+        exp = O.quantize_rows_q8_0(x, rows, k)
+        assert np.array_equal(got["d"], exp["d"]) and np.array_equal(got["qs"], exp["qs"])
+    with pytest.raises(vh.LengthMismatch):
+        rt.quantize_q8_0_into(xt, rows - 1, k, out)
+    small = rt.quantize_q8_0(rt.upload_f32(np.ones(64, np.float32)), 2, 32)
+    with pytest.raises(vh.LengthMismatch):
+        rt.quantize_q8_0_into(xt, rows, k, small)
 
 
 def test_q8_0_upload_download_every_int8_value(rt):

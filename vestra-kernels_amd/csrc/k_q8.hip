@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void quantize_tile_q8_0_kernel(const float *__
     constexpr int CB = 24;  // blocks per column chunk
     static_assert(R * CB * 8 % 256 == 0, "whole float4 per thread");
     __shared__ __attribute__((aligned(16))) uint32_t sq[CB][R][8];
-    __shared__ uint16_t sd[CB][R];
+    __shared__ __attribute__((aligned(16))) uint16_t sd[CB][R];
     const int tid = threadIdx.x, lane = tid & 63;
     const int r0 = blockIdx.x * R;
     const int nr = min(R, rows - r0);
@@ -109,9 +109,19 @@ __global__ __launch_bounds__(256) void quantize_tile_q8_0_kernel(const float *__
                     reinterpret_cast<const uint4 *>(&sq[jb][r][0])[half];
             }
         }
-        for (int u = tid; u < cb * R; u += 256) {
-            const int jb = u / R, r = u % R;
-            if (r < nr) dbits[(size_t)(j0 + jb) * rows + r0 + r] = sd[jb][r];
+        if (R == 8 && nr == R && (rows & 7) == 0 && (reinterpret_cast<uintptr_t>(dbits) & 15) == 0) {
+            // The 8 scales of a block column are 16 contiguous, aligned
+            // bytes: one store each instead of eight 2-byte stores (measured
+            // at 131072 x 768: 95 -> 84 us, the 2-byte stores alone had cost
+            // 11 us).
+            for (int jb = tid; jb < cb; jb += 256)
+                *reinterpret_cast<uint4 *>(dbits + (size_t)(j0 + jb) * rows + r0) =
+                    *reinterpret_cast<const uint4 *>(&sd[jb][0]);
+        } else {
+            for (int u = tid; u < cb * R; u += 256) {
+                const int jb = u / R, r = u % R;
+                if (r < nr) dbits[(size_t)(j0 + jb) * rows + r0 + r] = sd[jb][r];
+            }
         }
         __syncthreads();
     }

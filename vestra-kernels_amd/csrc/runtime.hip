@@ -1658,6 +1658,27 @@ extern "C" vh_status vh_quantize_q8_0(const vh_runtime *rt, const vh_tensor *x, 
     GUARD_END
 }
 
+extern "C" vh_status vh_quantize_q8_0_into(const vh_runtime *rt, const vh_tensor *x, size_t rows,
+                                           size_t k, vh_q8_tensor *out) {
+    NEED(rt, "vh_quantize_q8_0_into");
+    NEED(x, "vh_quantize_q8_0_into");
+    NEED(out, "vh_quantize_q8_0_into");
+    size_t n = 0;
+    if (k % 32 != 0)
+        return fail(VH_ERR_KERNEL, "vh_quantize_q8_0_into: k must be a multiple of 32, got " + std::to_string(k));
+    if (mul_overflows(rows, k, &n) || x->len != n || out->rows != rows || out->k != k)
+        return mismatch(x->len, out->rows * out->k, "x.len() must be out.len()*QK8_0");
+    if (out->rt != rt->s)
+        return fail(VH_ERR_KERNEL, "vh_quantize_q8_0_into: the output belongs to another runtime");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    return launch(s, "quantize_q8_0", [&] {
+        return vh::launch_quantize_q8_0(s.stream, x->ptr, out->qs, out->d, rows, k);
+    });
+    GUARD_END
+}
+
 extern "C" vh_status vh_gemm_q8_0(const vh_runtime *rt, const vh_q8_tensor *a_q,
                                   const vh_q8_tensor *b_q, size_t m, size_t n, size_t k,
                                   vh_tensor **out) {

@@ -185,6 +185,8 @@ unsafe extern "C" {
     fn vh_q8_tensor_k(t: *const VhQ8Tensor) -> usize;
     fn vh_quantize_q8_0(rt: *const VhRuntime, x: *const VhTensor, rows: usize, k: usize,
                         out: *mut *mut VhQ8Tensor) -> Status;
+    fn vh_quantize_q8_0_into(rt: *const VhRuntime, x: *const VhTensor, rows: usize, k: usize,
+                             out: *mut VhQ8Tensor) -> Status;
     fn vh_gemm_q8_0(rt: *const VhRuntime, a_q: *const VhQ8Tensor, b_q: *const VhQ8Tensor, m: usize, n: usize,
                     k: usize, out: *mut *mut VhTensor) -> Status;
 
@@ -690,6 +692,16 @@ impl HipRuntime {
         // SAFETY: live handles.
         self.call(|| unsafe { vh_quantize_q8_0(raw, x.raw, rows, k, &mut out) })?;
         Ok(HipQ8Tensor { raw: out, runtime: self.clone() })
+    }
+
+    /// quantize_row_q8_0(x, out) (src/q8_0_dot.rs:27-46) into an existing
+    /// [rows, k] Q8_0 tensor of this runtime.
+    pub fn quantize_q8_0_into(&self, x: &HipTensorF32, rows: usize, k: usize, out: &mut HipQ8Tensor)
+        -> Result<(), HipError> {
+        let raw = self.inner.raw;
+        let dst = out.raw;
+        // SAFETY: live handles; `out` is borrowed mutably for the call.
+        self.call(|| unsafe { vh_quantize_q8_0_into(raw, x.raw, rows, k, dst) })
     }
 
     /// Kernels::gemm_q8_0 (src/dispatch.rs:91-105) with b pre-transposed [n, k].

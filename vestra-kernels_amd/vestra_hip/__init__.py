@@ -129,6 +129,7 @@ SIGNATURES = [
     ("vh_q8_tensor_rows", _sz, [_p]),
     ("vh_q8_tensor_k", _sz, [_p]),
     ("vh_quantize_q8_0", _S, [_p, _p, _sz, _sz, _pp]),
+    ("vh_quantize_q8_0_into", _S, [_p, _p, _sz, _sz, _p]),
     ("vh_gemm_q8_0", _S, [_p, _p, _p, _sz, _sz, _sz, _pp]),
     ("vh_prepare_linear_q8_0", _S, [_p, _sz, _sz, _p, _f32p, _f32p, _pp]),
     ("vh_linear_q8_0_free", None, [_p]),
@@ -606,6 +607,10 @@ class Runtime:
         out = ctypes.c_void_p()
         _check(lib().vh_quantize_q8_0(self._h, x.handle, rows, k, ctypes.byref(out)))
         return Q8Tensor(self, out.value)
+
+    def quantize_q8_0_into(self, x: Tensor, rows, k, out: Q8Tensor) -> None:
+        """quantize_row_q8_0(x, out) into an existing rows x k Q8_0 tensor."""
+        _check(lib().vh_quantize_q8_0_into(self._h, x.handle, rows, k, out.handle))
 
     def gemm_q8_0(self, a_q: Q8Tensor, b_q: Q8Tensor, m, n, k) -> Tensor:
         return self._out(lib().vh_gemm_q8_0, a_q.handle, b_q.handle, m, n, k)
