@@ -480,11 +480,14 @@ def test_q8_0_upload_download_every_int8_value(rt):
 
 
 @pytest.mark.parametrize("m,n,k", [(865, 3072, 768), (8, 8, 64), (5, 17, 96), (64, 96, 3072),
-                                   (33, 70, 1056)])
+                                   (33, 70, 1056), (1024, 1920, 2112), (1024, 1920, 1120)])
 def test_gemm_q8_0_bit_exact(rt, m, n, k):
     """BASELINE config 4 (fc1 weights N(0, 0.02^2), activations N(0,1) quantised
-    on the device), the tests/q8_0_dot_matches_f32.rs shape, and K spanning
-    several 32-block scale chunks (3072) or ending in a one-block chunk (1056)."""
+    on the device), the tests/q8_0_dot_matches_f32.rs shape, and the scale
+    chunking and prefetch grouping: the 32x32 tile with 96 blocks in one
+    chunk (3072) and an odd block count (1056: one block per prefetch
+    group), the 64x64 tile with 66 blocks in chunks of 32, 32 and 2 (2112)
+    and with 35 blocks, odd, in chunks of 32 and 3 (1120)."""
     x = seeded.normal(91, m * k)
     w = seeded.normal(92, k * n, 0.02)
     wt = np.ascontiguousarray(w.reshape(k, n).T).reshape(-1)

@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) void layernorm_q8_0_kernel(const float *__rest
 // memory (clamped rows, no select) with a register prefetch QPF blocks
 // ahead, and the MFMAs of block b+1 are issued before the fold of block b,
 // so the matrix core works while the VALU folds.
-constexpr int QCH = 32;  // blocks per scale chunk (a multiple of the prefetch distance)
+
 
 // Epilogue of a Q8_0 projection, applied to the exact block-order sum with
 // separately rounded ops (the f32 ops the engine applies after
@@ -221,7 +221,7 @@ struct Q8Epi {
     uint16_t *q8_d;
 };
 
-template <Epi EPI, int FM, int FN>
+template <Epi EPI, int FM, int FN, int QPF>
 __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict__ a_qs,
                                                         const uint16_t *__restrict__ a_d,
                                                         const int8_t *__restrict__ b_qs,
@@ -230,9 +230,14 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
                                                         int K, Q8Epi ep) {
     static_assert(EPI != Epi::Qkv || FN == 2, "the QKV epilogue pairs fragments j = 0, 1");
     constexpr int TR = 32 * FM, TC = 32 * FN;  // workgroup tile
-    // Prefetch distance in blocks: 4 for the larger tiles; the 32x32 tile
-    // (16x16 per wave) measured 7-10% faster with 2 (fewer registers held).
-    constexpr int QPF = FM * FN == 1 ? 2 : 4;
+    // QCH: blocks per scale chunk.  The 32x32 tile (the narrow projections,
+    // K up to 3072) stages 96 blocks, so those are one chunk; the larger
+    // tiles stage 32 (K = 768 is one chunk), which keeps the staging
+    // registers at 16 per thread.  Later chunks wait for their scales with
+    // the operand prefetch drained, once per chunk.
+    // QPF: prefetch distance in blocks (q8_qpf), a divisor of the block
+    // count and of QCH.
+    constexpr int QCH = FM * FN == 1 ? 96 : 32;
     static_assert(QCH % QPF == 0, "scale chunks hold whole prefetch groups");
     __shared__ __attribute__((aligned(16))) float sa[QCH][TR];
     __shared__ __attribute__((aligned(16))) float sb[QCH][TC];
@@ -285,10 +290,11 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
             for (int j = 0; j < FN; j++)
                 is[i][j] = mfma16x16x32_i8(pa[slot][i], pb[slot][j], i32x4{0, 0, 0, 0});
     };
-    // Scales of one chunk, NA + NB per thread, loaded into registers a chunk
-    // ahead (all loads issued before any is waited on) and stored to LDS
-    // when the chunk starts.  Indices are clamped; stores past the chunk's
-    // last block are skipped.
+    // Scales of one chunk (up to QCH blocks), NA + NB per thread from
+    // clamped indices, all loads issued before any is waited on; stored to
+    // LDS as floats at the chunk's start.  Chunk 0's loads go out before
+    // the operand prefetch, so that the first wait for them leaves the
+    // prefetch in flight.
     constexpr int NA = TR * QCH / 256, NB = TC * QCH / 256;
     uint16_t ra[NA], rb[NB];
     auto load_scales = [&](int c) {
@@ -304,18 +310,7 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
             rb[t] = b_d[(size_t)(c + blk) * N + min(n0 + e % TC, N - 1)];
         }
     };
-    i32x4 cur[FM][FN];
-    if (nb > 0) {  // K == 0 stores zeros
-        load_scales(0);
-#pragma unroll
-        for (int p = 0; p < QPF; p++) fetch(p, p);
-        block_sums(0, cur);
-        fetch(QPF, 0);
-    }
-
-    for (int c0 = 0; c0 < nb; c0 += QCH) {
-        const int cn = min(QCH, nb - c0);
-        __syncthreads();  // previous chunk's scales are no longer read
+    auto store_scales = [&](int cn) {
 #pragma unroll
         for (int t = 0; t < NA; t++) {
             const int e = tid + 256 * t;
@@ -326,27 +321,56 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
             const int e = tid + 256 * t;
             if (e / TC < cn) sb[e / TC][e % TC] = half_bits_to_float(rb[t]);
         }
+    };
+    i32x4 cur[FM][FN];
+    if (nb > 0) {  // K == 0 stores zeros
+        load_scales(0);
+#pragma unroll
+        for (int p = 0; p < QPF; p++) fetch(p, p);
+        block_sums(0, cur);
+        fetch(QPF, 0);
+        // Chunk 0's scales, outside the chunk loop so that their wait
+        // leaves the operand prefetch in flight.
+        store_scales(min(QCH, nb));
+    }
+
+    for (int c0 = 0; c0 < nb; c0 += QCH) {
+        const int cn = min(QCH, nb - c0);  // a multiple of QPF (host check)
+        if (c0 > 0) {
+            __syncthreads();  // the previous chunk's scales are no longer read
+            load_scales(c0);
+            store_scales(cn);
+        }
         __syncthreads();
-        if (c0 + QCH < nb) load_scales(c0 + QCH);
         // Groups of QPF blocks with the prefetch slots fixed at compile time
-        // (QCH is a multiple of QPF, so block c0 + bl + u sits in slot u).
+        // (QPF divides the chunk, so block c0 + bl + u sits in slot u).  A
+        // group has no early exit and issues its loads in the same order
+        // as the prologue, so the wait before each block's MFMAs covers only
+        // that block's operands, QPF blocks after their loads went out.
+        // The scales of block bl + u are read from LDS one block ahead of
+        // its fold (past the chunk's last block, a clamped re-read).
+        auto read_scales = [&](int blk, f32x4 (&da)[FM], float (&db)[FN]) {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+                da[i] = *reinterpret_cast<const f32x4 *>(&sa[blk][wm * 16 * FM + i * 16 + 4 * lh]);
+#pragma unroll
+            for (int j = 0; j < FN; j++) db[j] = sb[blk][wn * 16 * FN + j * 16 + li];
+        };
+        f32x4 da[FM];
+        float db[FN];
+        read_scales(0, da, db);
         for (int bl = 0; bl < cn; bl += QPF) {
 #pragma unroll
             for (int u = 0; u < QPF; u++) {
-                if (bl + u >= cn) break;
                 const int b = c0 + bl + u;
                 // Block b+1 (slot (u+1) % QPF) goes to the matrix core first;
                 // past the last block it recomputes a clamped block, unused.
                 i32x4 nxt[FM][FN];
                 block_sums((u + 1) % QPF, nxt);
                 fetch(b + 1 + QPF, (u + 1) % QPF);
-                f32x4 da[FM];
-#pragma unroll
-                for (int i = 0; i < FM; i++)
-                    da[i] = *reinterpret_cast<const f32x4 *>(&sa[bl + u][wm * 16 * FM + i * 16 + 4 * lh]);
-                float db[FN];
-#pragma unroll
-                for (int j = 0; j < FN; j++) db[j] = sb[bl + u][wn * 16 * FN + j * 16 + li];
+                f32x4 da_n[FM];
+                float db_n[FN];
+                read_scales(min(bl + u + 1, cn - 1), da_n, db_n);
 #pragma unroll
                 for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -356,9 +380,13 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
                             acc[i][j][r] = add_rn(acc[i][j][r],
                                                   mul_rn(mul_rn(da[i][r], db[j]), (float)cur[i][j][r]));
 #pragma unroll
-                for (int i = 0; i < FM; i++)
+                for (int i = 0; i < FM; i++) {
+                    da[i] = da_n[i];
 #pragma unroll
                     for (int j = 0; j < FN; j++) cur[i][j] = nxt[i][j];
+                }
+#pragma unroll
+                for (int j = 0; j < FN; j++) db[j] = db_n[j];
             }
         }
     }
@@ -533,13 +561,32 @@ static void q8_tile(size_t m, size_t n, int *fm, int *fn) {
     *fm = *fn = tiles64 >= 480 ? 2 : 1;
 }
 
+// Prefetch distance in blocks: 2, lowered to 1 when the block count is odd
+// so that every prefetch group is whole (VESTRA_HIP_Q8_QPF=1|2|4 overrides
+// for A/B studies, again lowered to a divisor).  Measured on MI355X with
+// the loop's waits exact: 2 and 4 blocks ahead run within 2% of each other
+// (config-4 GEMM 19.1 vs 19.3 us, Q8_0 block 102.6 vs 103.6 us), and 2 keeps
+// the 64x64 tile at 118 VGPRs (4 waves per SIMD against 3); 8 ahead (176
+// VGPRs, 2 waves) took 23.1 us.
+static int q8_qpf(size_t nb) {
+    static const char *env = std::getenv("VESTRA_HIP_Q8_QPF");
+    int want = 2;
+    if (env && (env[0] == '1' || env[0] == '2' || env[0] == '4') && env[1] == 0) want = env[0] - '0';
+    for (int q = want; q > 1; q /= 2)
+        if (nb % q == 0) return q;
+    return 1;
+}
+
 template <Epi EPI, int FM, int FN>
 static void q8_launch(hipStream_t s, const int8_t *a_qs, const uint16_t *a_d, const int8_t *b_qs,
                       const uint16_t *b_d, float *c, size_t m, size_t n, size_t k,
                       const Q8Epi &ep) {
     dim3 grid((unsigned)((n + 32 * FN - 1) / (32 * FN)), (unsigned)((m + 32 * FM - 1) / (32 * FM)));
-    gemm_q8_0_kernel<EPI, FM, FN><<<grid, 256, 0, s>>>(a_qs, a_d, b_qs, b_d, c, (int)m, (int)n,
-                                                       (int)k, ep);
+    switch (q8_qpf(k / 32)) {
+        case 4: gemm_q8_0_kernel<EPI, FM, FN, 4><<<grid, 256, 0, s>>>(a_qs, a_d, b_qs, b_d, c, (int)m, (int)n, (int)k, ep); break;
+        case 2: gemm_q8_0_kernel<EPI, FM, FN, 2><<<grid, 256, 0, s>>>(a_qs, a_d, b_qs, b_d, c, (int)m, (int)n, (int)k, ep); break;
+        default: gemm_q8_0_kernel<EPI, FM, FN, 1><<<grid, 256, 0, s>>>(a_qs, a_d, b_qs, b_d, c, (int)m, (int)n, (int)k, ep); break;
+    }
 }
 
 template <Epi EPI>
