@@ -8,12 +8,15 @@ flash attention, out-projection+LayerScale+residual, LayerNorm, fc1+GELU,
 fc2+LayerScale+residual -- seven kernels on the runtime's stream.
 
 Timing: the block is prepared, then runs W untimed steps and K steps between
-two HIP events on the runtime's stream (vh_timer_start/stop): `value`.  A
-second pass of K steps with per-launch event profiling gives each kernel's
-average duration, from which the roofline fractions are computed with
-algorithmic FLOPs / bytes.  Started from an idle GPU, the clock needs about
-20 ms of the block's own continuous work to settle, so `steady_state`
-repeats both passes after 200 more untimed blocks.  The secondary sections
+two HIP events on the runtime's stream (vh_timer_start/stop), and a second
+pass of K steps with per-launch event profiling gives each kernel's average
+duration, from which the roofline fractions are computed with algorithmic
+FLOPs / bytes.  The GPU's clock is low when it starts from idle and settles
+within about 50 ms of continuous work (measured: W = 5, K = 20 take 192 us
+per block from idle and 164.5 us after 50-400 ms of blocks; half a second of
+idling brings the 189 us back).  Both passes therefore run twice: from the
+idle GPU right after preparation (`cold_start`), then after CLOCK_SETTLE_MS
+of untimed blocks (`value`, `kernels`, `roofline`).  The secondary sections
 follow (Q8_0 block, elementwise kernels, DPT head, BASELINE configs 4, 1, 2
 and 5).  The CPU baselines
 are the oracle's restatement of the crate's AVX-512 kernels (block, each
@@ -64,6 +67,9 @@ BYTES = {"layernorm": 2.0 * T * D * 4 + 2 * D * 4}
 
 
 TRAFFIC_SUMMARY = ROOT / "profiles" / "block_865_hbm_traffic.md"
+
+# Untimed blocks before the timed passes: the clock settles within ~50 ms.
+CLOCK_SETTLE_MS = 100.0
 
 
 def pct_peak(kernels: dict) -> float:
@@ -176,13 +182,25 @@ class BlockBench:
                  f"{entry.get('gbs', 0):7.1f} GB/s" if 'gbs' in entry else ""))
         return {"ms_per_step": ms, "kernels": kernels}
 
-    def steady(self, steps: int, extra: int = 200) -> dict:
-        """`extra` more untimed blocks (>= 30 ms of continuous GPU work, past
-        the clock's ramp), then the timed and profiled passes of run()."""
-        for _ in range(extra):
-            self.step()
-        out = self.run(steps, 0)
-        out["warmup_blocks"] = extra
+    def settle(self, ms: float) -> int:
+        """Untimed blocks for `ms` of wall time, synchronising every 20 so the
+        queue stays short: the GPU clock ramps over about 50 ms of continuous
+        work from idle.  Returns the number of blocks run."""
+        self.rt.synchronize()
+        t0, n = time.perf_counter(), 0
+        while (time.perf_counter() - t0) * 1e3 < ms:
+            for _ in range(20):
+                self.step()
+            n += 20
+            self.rt.synchronize()
+        return n
+
+    def steady(self, steps: int, warmup: int = 0) -> dict:
+        """The timed and profiled passes of run() after CLOCK_SETTLE_MS of
+        untimed blocks."""
+        blocks = self.settle(CLOCK_SETTLE_MS)
+        out = self.run(steps, warmup)
+        out["clock_settle"] = {"ms": CLOCK_SETTLE_MS, "blocks": blocks}
         return out
 
 
@@ -660,14 +678,15 @@ def main() -> int:
         print(json.dumps({args.only: section()}), flush=True)
         return 0
 
-    # value: W warm-up and K timed blocks right after preparation, from an
-    # idle GPU (the driver's scenario).  The clock needs ~20 ms of this
-    # block's own continuous work to settle, so the same K blocks are also
-    # timed after 200 more untimed blocks (steady_state).
+    # cold_start: W warm-up and K timed blocks right after preparation, from
+    # an idle GPU whose clock is still low.  value: the same W and K after
+    # CLOCK_SETTLE_MS of untimed blocks.  Both blocks are prepared first, so
+    # no host work separates the settle from the timed passes.
     f32_block, q8_block_bench = BlockBench(), BlockBench(q8_0=True)
-    gpu = f32_block.run(args.steps, args.warmup)
-    steady = f32_block.steady(args.steps)
-    log(f"steady state: {steady['ms_per_step'] * 1e3:.2f} us/block")
+    cold = f32_block.run(args.steps, args.warmup)
+    log(f"cold start: {cold['ms_per_step'] * 1e3:.2f} us/block")
+    gpu = f32_block.steady(args.steps, args.warmup)
+    log(f"after {CLOCK_SETTLE_MS:.0f} ms of untimed blocks: {gpu['ms_per_step'] * 1e3:.2f} us/block")
     q8_block = q8_block_bench.run(max(10, min(args.steps, 100)), args.warmup)
     elementwise = gpu_elementwise()
     dpt = gpu_dpt()
@@ -717,12 +736,13 @@ def main() -> int:
                                "FETCH_SIZE / WRITE_SIZE summary of this block, not measured "
                                "in this run"),
         },
-        "timing": ("W warm-up then K timed blocks right after preparation, from an idle GPU "
-                   "whose clock is still ramping; steady_state repeats K blocks after 200 more"),
-        "steady_state": {"us_per_block": round(steady["ms_per_step"] * 1e3, 2),
-                         "extra_warmup_blocks": steady["warmup_blocks"],
-                         "gemm_attn_pct_fp32_mfma_peak": pct_peak(steady["kernels"]),
-                         "kernels": steady["kernels"]},
+        "timing": (f"W warm-up then K timed blocks after {CLOCK_SETTLE_MS:.0f} ms of untimed blocks "
+                   "(clock_settle), which bring the GPU clock from its idle level to steady; "
+                   "cold_start is the same W and K right after preparation from the idle GPU"),
+        "clock_settle": gpu["clock_settle"],
+        "cold_start": {"us_per_block": round(cold["ms_per_step"] * 1e3, 2),
+                       "gemm_attn_pct_fp32_mfma_peak": pct_peak(cold["kernels"]),
+                       "kernels": cold["kernels"]},
         "kernels": ker,
         "config1_2_standalone": configs,
         "q8_0": q8,

@@ -811,6 +811,15 @@ struct Tile {
     int bm, bn, bk, wm, wn;
 };
 
+// XCD-grouped tile order (tile_of_block): on above 1024 rows, where the
+// operand panels outgrow what the XCDs' L2s share; VESTRA_HIP_GEMM_XCD=0|1
+// forces it off or on (A/B studies).
+int use_xcd_order(size_t m) {
+    static const char *env = std::getenv("VESTRA_HIP_GEMM_XCD");
+    if (env && (env[0] == '0' || env[0] == '1') && env[1] == 0) return env[0] - '0';
+    return m > 1024;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, int CONV = 0>
 hipError_t launch_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int splits, int kps) {
     constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 4) * sizeof(float);
@@ -818,7 +827,7 @@ hipError_t launch_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int 
     static std::atomic<uint64_t> configured{0};
     if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
     dim3 grid((unsigned)((g.n + BN - 1) / BN), (unsigned)((g.m + BM - 1) / BM), (unsigned)splits);
-    const int xcd_order = g.m > 1024;
+    const int xcd_order = use_xcd_order(g.m);
     kernel<<<grid, WM * WN * 64, lds, s>>>(g.a, g.bt, (int)g.m, (int)g.n, (int)g.k, kps, xcd_order, ep);
     return hipGetLastError();
 }
@@ -971,7 +980,7 @@ hipError_t launch_tail(hipStream_t s, const GemmArgs &g, EpiArgs ep, const TailP
     ep.tail_count = p.count;
     ep.tail_kps = (int)g.k / p.splits;
     const unsigned blocks = (unsigned)(p.full + p.splits * ((p.count + 7) / 8 * 8));
-    const int xcd_order = g.m > 1024;
+    const int xcd_order = use_xcd_order(g.m);
     kernel<<<blocks, WM * WN * 64, lds, s>>>(g.a, g.bt, (int)g.m, (int)g.n, (int)g.k, (int)g.k, xcd_order, ep);
     return hipGetLastError();
 }
