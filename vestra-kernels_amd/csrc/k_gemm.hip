@@ -928,6 +928,8 @@ struct TailPlan {
 // after them as S pieces of K / S each brings the busiest CU's load from
 // ceil(T / C) tiles to T / C rounded down plus ceil(S (T % C) / C) / S.  S is
 // the smallest of 2..4 with the lowest load (pieces of at least 4 slices).
+// With fewer tiles than CUs there is no whole round and every tile runs as
+// pieces (the 865 x 768 x 768 projection: 168 tiles, 504 pieces).
 // VESTRA_HIP_GEMM_TAIL=0 turns the tail off and =1 takes it whenever it
 // lowers the load at all (A/B studies and tests).
 bool tail_plan(const GemmArgs &g, const Tile &t, TailPlan *plan) {
@@ -941,7 +943,7 @@ bool tail_plan(const GemmArgs &g, const Tile &t, TailPlan *plan) {
     const long tiles = (long)((g.m + 63) / 64) * (long)((g.n + 63) / 64);
     const long full = tiles / cus * cus, rem = tiles - full;
     const long count8 = (rem + 7) / 8 * 8;
-    if (full == 0 || rem == 0 || full % 8 != 0) return false;
+    if (rem == 0 || full % 8 != 0) return false;
     const long ktiles = (long)(g.k / 32);
     // Measured on MI355X (fc1-shaped, N = 3072, K = 768, per-launch events,
     // tail off -> on): M = 512 38.5 -> 32.6 us, 832 51.8 -> 46.1, 865 52.4 ->
