@@ -76,23 +76,31 @@ def test_conv2d_hand_checked_and_one_shot(rt):
 @pytest.mark.parametrize("in_c, out_c, ih, iw, k, s, p", [c for c in CONV_CASES if c[0] % 32 == 0])
 def test_conv2d_direct_matches_staged(rt, monkeypatch, in_c, out_c, ih, iw, k, s, p):
     """The direct implicit GEMM (CHW image read in place) against the staged
-    forms (padded channel-last copy, patch matrix, transposes): the same
-    products in the same k order, so stride-1 shapes agree bit for bit; the
-    staged stride-2 form splits K and agrees to rounding."""
+    forms (padded channel-last copy, patch matrix, transposes): with whole
+    tiles (the GEMM's balanced tail off) they take the same products in the
+    same k order, so stride-1 shapes agree bit for bit; the staged stride-2
+    form splits K and agrees to rounding.  By default a staged GEMM with
+    fewer tiles than CUs runs its tiles as K pieces (the 1x1 768 -> 96
+    convolution: 28 tiles), which also agrees to rounding."""
     x, w, b = _data(0xD1EC7 + in_c + k, in_c * ih * iw, out_c * in_c * k * k, out_c)
     w = w * np.float32(1.0 / np.sqrt(in_c * k * k))
     conv = rt.prepare_conv2d_f32(in_c, out_c, k, k, s, p, w, b)
     xt = rt.upload_f32(x)
     outs = {}
-    for direct in ("1", "0"):
+    for direct, tail in (("1", "0"), ("0", "0"), ("0", None)):
         monkeypatch.setenv("VESTRA_HIP_CONV_DIRECT", direct)
-        outs[direct] = (rt.download_f32(conv.run(xt, ih, iw)),
-                        rt.download_f32(conv.run_relu_input(xt, ih, iw)))
-    for a, b_ in zip(outs["1"], outs["0"]):
+        if tail is None:
+            monkeypatch.delenv("VESTRA_HIP_GEMM_TAIL", raising=False)
+        else:
+            monkeypatch.setenv("VESTRA_HIP_GEMM_TAIL", tail)
+        outs[(direct, tail)] = (rt.download_f32(conv.run(xt, ih, iw)),
+                                rt.download_f32(conv.run_relu_input(xt, ih, iw)))
+    for a, b_, t in zip(outs[("1", "0")], outs[("0", "0")], outs[("0", None)]):
         if s == 1:
             assert_bits_equal(a, b_, "direct vs staged convolution")
         else:
             assert max_rel(a, b_) <= 1e-5
+        assert max_rel(a, t) <= 1e-5
 
 
 @pytest.mark.parametrize("in_c", [32, 12])  # direct implicit GEMM / channel-last patch copy
