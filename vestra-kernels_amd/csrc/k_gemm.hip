@@ -2,12 +2,20 @@
 //
 // C[m,n] = sum_k A[m,k] * Bt[n,k]; A is the activation (row-major), Bt the
 // weight prepared once in [out, in] order so both operands stream k-contiguous
-// rows.  A workgroup of WM x WN wave64s owns a BM x BN tile; BK-wide slices of
-// A and Bt are double-buffered in LDS with rows padded by 4 floats (16-byte
-// fragment reads of 16 consecutive rows then touch 64 distinct banks).  Each
-// wave computes a (BM/WM) x (BN/WN) sub-tile with v_mfma_f32_16x16x4_f32: one
-// ds_read_b128 per 16-row fragment feeds four MFMA k-steps (lane group h
-// supplies k = kk+4h+s at step s).
+// rows.  A workgroup of WM x WN wave64s owns a BM x BN tile and stages BK-wide
+// slices of A and Bt in LDS (double-buffered, staged through registers).  A
+// slice row is BK floats with no padding; its 16-byte granule g is stored at
+// granule g ^ (row % (BK / 4)).  A fragment read (lane l: row l % 16 plus a
+// multiple of 16, granule kk/4 + l / 16) then spreads the rows a 16-byte LDS
+// access serves together over distinct granules, and so do the slice stores
+// (lane l: row l / (BK/4), granule l % (BK/4)).  Measured with
+// SQ_LDS_BANK_CONFLICT on MI355X: 0 for this layout at BK = 32 and 64; the
+// rows-padded-by-4 layout it replaces conflicted as often as it issued
+// MFMAs, and swizzling by row % 8 alone still conflicted at BK = 64.  Each
+// wave computes a (BM/WM) x
+// (BN/WN) sub-tile with v_mfma_f32_16x16x4_f32: one ds_read_b128 per 16-row
+// fragment feeds four MFMA k-steps (lane group h supplies k = kk+4h+s at
+// step s).
 //
 // Split-K (grid.z > 1) is deterministic: each split writes its partial tile
 // to a workspace and a reduction kernel sums the partials in split order
@@ -142,6 +150,19 @@ __device__ __forceinline__ int tail_tile_of_block(const EpiArgs &ep, bool xcd_or
     return 0;
 }
 
+// Float offset of granule g (4 floats) of slice row r: rows of BK floats,
+// granules XOR-swizzled by the row (BK / 4 granules per row, BK >= 32).
+template <int BK>
+__device__ __forceinline__ int swz(int r, int g) {
+    static_assert(BK % 32 == 0, "a slice row holds at least 8 granules");
+    return r * BK + 4 * (g ^ (r & (BK / 4 - 1)));
+}
+
+template <int BM, int BN, int BK>
+constexpr size_t gemm_lds_bytes() {
+    return 2 * (size_t)(BM + BN) * BK * sizeof(float);
+}
+
 // EXACT: K and the split length are multiples of BK and K % 4 == 0, so every
 // k-slice is whole.  Rows past M (columns past N) load a clamped in-range row
 // and are NOT zeroed: C[m][n] depends only on A row m and Bt row n, and rows
@@ -168,7 +189,6 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                                                               int k_per_split, int xcd_order,
                                                               EpiArgs ep) {
     constexpr int NT = WM * WN * 64;
-    constexpr int LDK = BK + 4;
     constexpr int CPR = BK / 4;  // float4 chunks per row slice
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 16, FN = TN / 16;
@@ -180,9 +200,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     static_assert(EPI != Epi::Qkv || TN == 32 || TN == 64,
                   "QKV epilogue needs whole 32-wide RoPE halves of one head per wave tile");
 
+    // LDS buffer b: A slice [BM][BK], then Bt slice [BN][BK].
+    constexpr int STAGE = (BM + BN) * BK;
     extern __shared__ __attribute__((aligned(16))) float smem[];
-    float *As = smem;                    // [2][BM * LDK]
-    float *Bs = smem + 2 * BM * LDK;     // [2][BN * LDK]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lh = lane >> 4;
@@ -295,12 +315,12 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
         }
     };
     auto lstore = [&](int buf) {
-        float *as = As + buf * BM * LDK;
-        float *bs = Bs + buf * BN * LDK;
+        float *as = smem + buf * STAGE;
+        float *bs = as + BM * BK;
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
-            int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
-            *reinterpret_cast<f32x4 *>(&as[row * LDK + kq]) = ra[i];
+            int c = tid + i * NT;
+            *reinterpret_cast<f32x4 *>(&as[swz<BK>(c / CPR, c % CPR)]) = ra[i];
         }
         if constexpr (CONV == 3) {
             // Pixel cd_p, channels 8 cd_cg .. +7 of the slice: ReLU on the
@@ -313,13 +333,13 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                     if (ep.cd_relu) v[e] = fmaxf(v[e], 0.0f);
                     v[e] = cd_ok ? v[e] : 0.0f;
                 }
-                *reinterpret_cast<f32x4 *>(&bs[cd_p * LDK + 8 * cd_cg + 4 * i]) = v;
+                *reinterpret_cast<f32x4 *>(&bs[swz<BK>(cd_p, 2 * cd_cg + i)]) = v;
             }
         } else {
 #pragma unroll
             for (int i = 0; i < BCH; i++) {
-                int c = tid + i * NT, row = c / CPR, kq = (c % CPR) * 4;
-                *reinterpret_cast<f32x4 *>(&bs[row * LDK + kq]) = rb[i];
+                int c = tid + i * NT;
+                *reinterpret_cast<f32x4 *>(&bs[swz<BK>(c / CPR, c % CPR)]) = rb[i];
             }
         }
     };
@@ -330,32 +350,39 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // Fragment i (A) / j (Bt) of k-step kk from buffer buf: rows wm*TM + 16i + li
+    // (wn*TN + 16j + li), granule kk/4 + lh, i.e. swz(row, kk/4 + lh).  The
+    // rows of a lane are li plus multiples of 16, so the swizzle depends on
+    // li alone: one per-lane offset per k-step, and everything else is an
+    // immediate.
+    int goff[BK / 16];
+#pragma unroll
+    for (int q = 0; q < BK / 16; q++) goff[q] = 4 * ((4 * q + lh) ^ (li & (CPR - 1)));
+    f32x4 a[2][FM], b[2][FN];
+    auto fetch = [&](int slot, int buf, int kk) {
+        const float *as = smem + buf * STAGE + (wm * TM + li) * BK + goff[kk / 16];
+        const float *bs = smem + buf * STAGE + BM * BK + (wn * TN + li) * BK + goff[kk / 16];
+#pragma unroll
+        for (int i = 0; i < FM; i++) a[slot][i] = *reinterpret_cast<const f32x4 *>(as + i * 16 * BK);
+#pragma unroll
+        for (int j = 0; j < FN; j++) b[slot][j] = *reinterpret_cast<const f32x4 *>(bs + j * 16 * BK);
+    };
+    auto mstep = [&](int cur, int s) {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++) acc[i][j] = mfma16x16x4(a[cur][i][s], b[cur][j][s], acc[i][j]);
+    };
     // Fragments of k-step kk+16 are read from LDS while the MFMAs of k-step
     // kk run (register double buffering).
     auto compute = [&](int buf) {
-        const float *as = As + buf * BM * LDK + (wm * TM + li) * LDK + 4 * lh;
-        const float *bs = Bs + buf * BN * LDK + (wn * TN + li) * LDK + 4 * lh;
-        f32x4 a[2][FM], b[2][FN];
-        auto fetch = [&](int slot, int kk) {
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-                a[slot][i] = *reinterpret_cast<const f32x4 *>(&as[i * 16 * LDK + kk]);
-#pragma unroll
-            for (int j = 0; j < FN; j++)
-                b[slot][j] = *reinterpret_cast<const f32x4 *>(&bs[j * 16 * LDK + kk]);
-        };
-        fetch(0, 0);
+        fetch(0, buf, 0);
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 16) {
             const int cur = (kk / 16) & 1;
-            if (kk + 16 < BK) fetch(cur ^ 1, kk + 16);
+            if (kk + 16 < BK) fetch(cur ^ 1, buf, kk + 16);
 #pragma unroll
-            for (int s = 0; s < 4; s++)
-#pragma unroll
-                for (int i = 0; i < FM; i++)
-#pragma unroll
-                    for (int j = 0; j < FN; j++)
-                        acc[i][j] = mfma16x16x4(a[cur][i][s], b[cur][j][s], acc[i][j]);
+            for (int s = 0; s < 4; s++) mstep(cur, s);
         }
     };
 
@@ -369,9 +396,10 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
         // basic block and its instruction order can be pinned: the fragment
         // reads of k-step s+1 and the LDS stores of the next slice issue in
         // the shadow of the MFMAs of k-step s, and the global loads of the
-        // next slice go out first.
-        for (int t = 0; t < ktiles; t++) {
-            const int cur = t & 1;
+        // next slice go out first.  Unrolled by two, so that the buffer of
+        // each slice is a constant and every LDS address is a loop-invariant
+        // register plus an immediate.
+        auto slice = [&](int t, int cur) {
             gload(kbeg + min(t + 1, ktiles - 1) * BK);
             compute(cur);
             lstore(cur ^ 1);
@@ -396,7 +424,13 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
             __builtin_amdgcn_sched_group_barrier(0x008, NM - NW, 0);
             __builtin_amdgcn_sched_group_barrier(0x200, NL - NW, 0);
             __syncthreads();
+        };
+        int t = 0;
+        for (; t + 1 < ktiles; t += 2) {
+            slice(t, 0);
+            slice(t + 1, 1);
         }
+        if (t < ktiles) slice(t, 0);
     } else {
         for (int t = 0; t < ktiles; t++) {
             const int cur = t & 1;
@@ -822,7 +856,7 @@ int use_xcd_order(size_t m) {
 
 template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, int CONV = 0>
 hipError_t launch_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int splits, int kps) {
-    constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 4) * sizeof(float);
+    constexpr size_t lds = gemm_lds_bytes<BM, BN, BK>();
     auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, SPLIT, EXACT, CONV>;
     static std::atomic<uint64_t> configured{0};
     if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
@@ -971,7 +1005,7 @@ bool tail_plan(const GemmArgs &g, const Tile &t, TailPlan *plan) {
 template <Epi EPI>
 hipError_t launch_tail(hipStream_t s, const GemmArgs &g, EpiArgs ep, const TailPlan &p) {
     constexpr int BM = 64, BN = 64, BK = 32, WM = 2, WN = 2;
-    constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 4) * sizeof(float);
+    constexpr size_t lds = gemm_lds_bytes<BM, BN, BK>();
     auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, false, true, 0, true>;
     static std::atomic<uint64_t> configured{0};
     if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
