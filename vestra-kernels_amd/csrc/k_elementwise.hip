@@ -177,21 +177,24 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float *__restrict_
     float *y = out + row * cols;
     if ((cols & 3) == 0 && cols <= 1024 && ((((uintptr_t)x) | ((uintptr_t)y)) & 15) == 0) {
         const int n4 = (int)(cols >> 2);
-        f32x4 r[4];
+        // Every read (the row, gamma, beta) is issued before the statistics:
+        // gamma and beta come from clamped indices (chunks past the row end
+        // read chunk 0 and are dropped), so that no load waits behind the
+        // bounds branch of its store.
+        f32x4 r[4], g[4], b[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            int idx = lane + j * 64;
+            const int idx = lane + j * 64, ci = idx < n4 ? idx : 0;
             r[j] = idx < n4 ? ld<NT>(reinterpret_cast<const f32x4 *>(x) + idx) : f32x4{0, 0, 0, 0};
+            g[j] = reinterpret_cast<const f32x4 *>(gamma)[ci];
+            b[j] = reinterpret_cast<const f32x4 *>(beta)[ci];
         }
         float mean, inv;
         ln_row_stats(r, lane, n4, (int)cols, eps, mean, inv);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            int idx = lane + j * 64;
-            if (idx < n4)
-                st<NT>(reinterpret_cast<f32x4 *>(y) + idx,
-                       ln_apply(r[j], mean, inv, reinterpret_cast<const f32x4 *>(gamma)[idx],
-                                reinterpret_cast<const f32x4 *>(beta)[idx]));
+            const int idx = lane + j * 64;
+            if (idx < n4) st<NT>(reinterpret_cast<f32x4 *>(y) + idx, ln_apply(r[j], mean, inv, g[j], b[j]));
         }
     } else {
         float s = 0.0f;

@@ -144,11 +144,15 @@ __global__ __launch_bounds__(256) void layernorm_q8_0_kernel(const float *__rest
     if (row >= rows) return;
     const f32x4 *x = reinterpret_cast<const f32x4 *>(in + (size_t)row * cols);
     const int n4 = cols >> 2;
-    f32x4 r[4];
+    // The row, gamma and beta (clamped indices) are all read before the
+    // statistics, so the loads are in flight together.
+    f32x4 r[4], g[4], b[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int idx = lane + j * 64;
+        const int idx = lane + j * 64, gi = min(idx, n4 - 1);
         r[j] = idx < n4 ? x[idx] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        g[j] = reinterpret_cast<const f32x4 *>(gamma)[gi];
+        b[j] = reinterpret_cast<const f32x4 *>(beta)[gi];
     }
     float mean, inv;
     ln_row_stats(r, lane, n4, cols, eps, mean, inv);
@@ -156,9 +160,7 @@ __global__ __launch_bounds__(256) void layernorm_q8_0_kernel(const float *__rest
     for (int j = 0; j < 4; j++) {
         const int idx = lane + j * 64;
         const bool live = idx < n4;  // whole 8-lane groups, as n4 % 8 == 0
-        const int gi = min(idx, n4 - 1);
-        const f32x4 y = ln_apply(r[j], mean, inv, reinterpret_cast<const f32x4 *>(gamma)[gi],
-                                 reinterpret_cast<const f32x4 *>(beta)[gi]);
+        const f32x4 y = ln_apply(r[j], mean, inv, g[j], b[j]);
         float amax = 0.0f;
 #pragma unroll
         for (int e = 0; e < 4; e++) amax = q8_absmax(amax, y[e]);
