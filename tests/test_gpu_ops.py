@@ -139,8 +139,10 @@ def test_errors_before_launch(rt):
 
 # ---- GEMM (fp32 MFMA) -------------------------------------------------------
 
+# (70, 100, 2304) and (70, 3000, 768) take the 64 x 128 x 64 tile with K not a
+# multiple of 64 (the masked slice path of the BK = 64 swizzled layout).
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 5, 3), (865, 768, 768), (33, 96, 130),
-                                   (64, 32, 64), (129, 67, 257)])
+                                   (64, 32, 64), (129, 67, 257), (70, 100, 2304), (70, 3000, 768)])
 def test_gemm_row_major_matches_float64(rt, m, k, n):
     a = seeded.normal(101 + m, m * k)
     b = seeded.normal(202 + n, k * n)
