@@ -29,6 +29,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <type_traits>
 
 #include "common.h"
 #include "kernels.h"
@@ -685,30 +686,46 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                         resid[i][j][r] = ep.c[row * N + min(cbase + j * 16, N - 1)];
                     }
         }
+        // A tile wholly inside C and, for GELU, wholly before the scalar
+        // tail (the last n % 16 values, tail_start on) stores without
+        // per-element checks; the decision is per tile, so the branch is
+        // uniform and the arithmetic is the same either way.
+        auto store_all = [&](auto whole_tile) {
+            constexpr bool WHOLE = decltype(whole_tile)::value;
 #pragma unroll
-        for (int j = 0; j < FN; j++) {
-            const int col = cbase + j * 16;
-            if (col >= N) continue;
+            for (int j = 0; j < FN; j++) {
+                const int col = cbase + j * 16;
+                if (!WHOLE && col >= N) continue;
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+                for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int row = rbase + i * 16 + r;
-                    if (row >= M) continue;
-                    const size_t idx = (size_t)row * N + col;
-                    float v = acc[i][j][r];
-                    if (ep.bias) v = add_rn(v, bias[j]);
-                    if constexpr (EPI == Epi::Store) {
-                        if (ep.gamma) v = mul_rn(v, gamma[j]);
-                        ep.c[idx] = v;
-                    } else if constexpr (EPI == Epi::Gelu) {
-                        ep.c[idx] = idx < ep.tail_start ? gelu_avx512_form(v) : gelu_scalar_form(v);
-                    } else {
-                        if (ep.gamma) v = mul_rn(v, gamma[j]);
-                        ep.c[idx] = add_rn(resid[i][j][r], v);
+                    for (int r = 0; r < 4; r++) {
+                        const int row = rbase + i * 16 + r;
+                        if (!WHOLE && row >= M) continue;
+                        const size_t idx = (size_t)row * N + col;
+                        float v = acc[i][j][r];
+                        if (ep.bias) v = add_rn(v, bias[j]);
+                        if constexpr (EPI == Epi::Store) {
+                            if (ep.gamma) v = mul_rn(v, gamma[j]);
+                            ep.c[idx] = v;
+                        } else if constexpr (EPI == Epi::Gelu) {
+                            if constexpr (WHOLE)
+                                ep.c[idx] = gelu_avx512_form(v);
+                            else
+                                ep.c[idx] = idx < ep.tail_start ? gelu_avx512_form(v) : gelu_scalar_form(v);
+                        } else {
+                            if (ep.gamma) v = mul_rn(v, gamma[j]);
+                            ep.c[idx] = add_rn(resid[i][j][r], v);
+                        }
                     }
-                }
-        }
+            }
+        };
+        const bool whole = m0 + BM <= M && n0 + BN <= N &&
+                           (EPI != Epi::Gelu || (size_t)(m0 + BM - 1) * N + (n0 + BN - 1) < ep.tail_start);
+        if (whole)
+            store_all(std::true_type{});
+        else
+            store_all(std::false_type{});
     }
 }
 
