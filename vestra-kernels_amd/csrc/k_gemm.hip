@@ -1044,7 +1044,9 @@ hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     if (!tile_override(&t, &splits)) default_tile(g, &t, &splits);
     if (EPI == Epi::Qkv) splits = 1;
     if (splits > 1 && (g.ws == nullptr || g.ws_floats < (size_t)splits * g.m * g.n)) splits = 1;
-    if constexpr (EPI == Epi::Store || EPI == Epi::Gelu) {
+    if constexpr (EPI != Epi::Qkv) {
+        // Store, GELU and Residual: the last piece of a tail tile runs the
+        // epilogue once (a Residual tile adds its residual exactly once).
         TailPlan p;
         if (splits == 1 && tail_plan(g, t, &p)) return launch_tail<EPI>(s, g, ep, p);
     }
