@@ -140,9 +140,12 @@ def test_errors_before_launch(rt):
 # ---- GEMM (fp32 MFMA) -------------------------------------------------------
 
 # (70, 100, 2304) and (70, 3000, 768) take the 64 x 128 x 64 tile with K not a
-# multiple of 64 (the masked slice path of the BK = 64 swizzled layout).
+# multiple of 64 (the masked slice path of the BK = 64 swizzled layout);
+# (70, 2112, 768) whole 64-wide slices in an odd count per split (the slice
+# loop runs two slices per iteration plus one).
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 5, 3), (865, 768, 768), (33, 96, 130),
-                                   (64, 32, 64), (129, 67, 257), (70, 100, 2304), (70, 3000, 768)])
+                                   (64, 32, 64), (129, 67, 257), (70, 100, 2304), (70, 3000, 768),
+                                   (70, 2112, 768)])
 def test_gemm_row_major_matches_float64(rt, m, k, n):
     a = seeded.normal(101 + m, m * k)
     b = seeded.normal(202 + n, k * n)
@@ -193,13 +196,14 @@ def test_fc1_gelu_epilogue_vs_oracle(rt, m):
 
 
 @pytest.mark.parametrize("m,k,n", [(865, 768, 3072), (400, 768, 3072), (865, 768, 3136),
-                                   (300, 256, 4096), (3460, 768, 3072)])
+                                   (300, 256, 4096), (3460, 768, 3072), (865, 480, 3072)])
 def test_gemm_balanced_tail(rt, monkeypatch, m, k, n):
     """The tiles past the last whole round over the CUs run as K pieces that
     the last piece to finish sums in piece order (64 x 64 tile, GELU
     epilogue).  Shapes: fc1 (672 tiles, 3 pieces), 336 tiles (3 pieces), 686
     tiles (4 pieces, tail padded to a multiple of 8), K = 256 (2 pieces), the
-    batched fc1 (2640 tiles, XCD-ordered).  Bars: identical run to run, and
+    batched fc1 (2640 tiles, XCD-ordered), K = 480 (3 pieces of 5 slices: an
+    odd slice count per piece).  Bars: identical run to run, and
     within 1e-5 of the one-workgroup-per-tile grid, from which the tail's
     K-split sums must differ in some bits (the tail ran)."""
     a = rt.upload_f32(seeded.normal(41 + m, m * k))
