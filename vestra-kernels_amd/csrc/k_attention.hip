@@ -361,6 +361,24 @@ __device__ __forceinline__ void copy_to_lds16(const float *src, float *lds_wave)
     __builtin_amdgcn_global_load_lds((global_ptr)src, (lds_ptr)lds_wave, 16, 0, 0);
 }
 
+// max(v, value of the lane 16 (32) away) on the VALU: gfx950's
+// v_permlane16_swap (v_permlane32_swap) of two copies of v leaves v in one
+// and the partner lane's v in the other (in either order, and fmaxf does not
+// depend on the order), without the LDS round trip of a shuffle.  Written
+// out because the compiler's builtins for these instructions, given a value
+// and its own copy, used one result twice; s_nop 1 on each side covers the
+// VALU-write / permlane hazards.
+__device__ __forceinline__ float max_xor16(float v) {
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float max_xor32(float v) {
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return fmaxf(a, b);
+}
+
 template <bool TOKEN_MAJOR, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_direct_kernel(
     FlashArgs fa) {
@@ -472,8 +490,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     mx = fmaxf(mx, s[g][r]);
                 }
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mx = max_xor32(max_xor16(mx));
         const float mnew = fmaxf(m, mx * scale);
         // A range with no valid key yet keeps m = -inf; 0 as the reference
         // makes exp2 see -inf (giving 0), never NaN.
