@@ -862,13 +862,22 @@ struct Tile {
     int bm, bn, bk, wm, wn;
 };
 
-// XCD-grouped tile order (tile_of_block): on above 1024 rows, where the
-// operand panels outgrow what the XCDs' L2s share; VESTRA_HIP_GEMM_XCD=0|1
-// forces it off or on (A/B studies).
-int use_xcd_order(size_t m) {
+// XCD-grouped tile order (tile_of_block), by shape, from FETCH_SIZE /
+// WRITE_SIZE counters and kernel traces on MI355X:
+// - past 1024 rows, where the operand panels outgrow what the XCDs' L2s
+//   share (fc2 at M = 3460: 148 -> 140 us);
+// - long K (fc2 at 865 tokens, split K): 105 -> 50 MB fetched and written,
+//   time unchanged;
+// - 3072 columns and more (fc1 at 865 tokens): 43.8 -> 43.2 us;
+// and not for QKV and the out-projection at 865 tokens, which fetch less
+// with it but ran 0.3-0.4 us slower.  The convolution and patch-scatter
+// GEMMs keep the row rule.  VESTRA_HIP_GEMM_XCD=0|1 forces it off or on (A/B
+// studies).
+int use_xcd_order(const GemmArgs &g) {
     static const char *env = std::getenv("VESTRA_HIP_GEMM_XCD");
     if (env && (env[0] == '0' || env[0] == '1') && env[1] == 0) return env[0] - '0';
-    return m > 1024;
+    if (g.conv_in_c || g.scatter_kw) return g.m > 1024;
+    return g.m > 1024 || g.k >= 2048 || g.n >= 3072;
 }
 
 template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, int CONV = 0>
@@ -878,7 +887,7 @@ hipError_t launch_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int 
     static std::atomic<uint64_t> configured{0};
     if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
     dim3 grid((unsigned)((g.n + BN - 1) / BN), (unsigned)((g.m + BM - 1) / BM), (unsigned)splits);
-    const int xcd_order = use_xcd_order(g.m);
+    const int xcd_order = use_xcd_order(g);
     kernel<<<grid, WM * WN * 64, lds, s>>>(g.a, g.bt, (int)g.m, (int)g.n, (int)g.k, kps, xcd_order, ep);
     return hipGetLastError();
 }
@@ -1032,7 +1041,7 @@ hipError_t launch_tail(hipStream_t s, const GemmArgs &g, EpiArgs ep, const TailP
     ep.tail_count = p.count;
     ep.tail_kps = (int)g.k / p.splits;
     const unsigned blocks = (unsigned)(p.full + p.splits * ((p.count + 7) / 8 * 8));
-    const int xcd_order = use_xcd_order(g.m);
+    const int xcd_order = use_xcd_order(g);
     kernel<<<blocks, WM * WN * 64, lds, s>>>(g.a, g.bt, (int)g.m, (int)g.n, (int)g.k, (int)g.k, xcd_order, ep);
     return hipGetLastError();
 }
