@@ -125,8 +125,9 @@ __device__ __forceinline__ void tile_of_block(bool xcd_order, int &tm, int &tn, 
 // TAIL grids are one-dimensional: workgroups [0, tail_full) take the whole
 // tiles (tail_full % 8 == 0; with xcd_order renumbered as above), and the
 // rest the K pieces of the tail tiles, numbered so that the tail_splits
-// pieces of one tile share bid % 8, i.e. one XCD and its L2.  Tail indices
-// past tail_count (padding to a multiple of 8) return -1.
+// pieces of one tile share bid % 8, i.e. one XCD and its L2 (with xcd_order
+// each XCD's tail tiles are also consecutive in tile_walk order).  Tail
+// indices past tail_count (padding to a multiple of 8) return -1.
 __device__ __forceinline__ int tail_tile_of_block(const EpiArgs &ep, bool xcd_order, int nx, int ny,
                                                   int &tm, int &tn, int &piece, int &u) {
     const int bid = blockIdx.x;
@@ -138,7 +139,10 @@ __device__ __forceinline__ int tail_tile_of_block(const EpiArgs &ep, bool xcd_or
     } else {
         const int q = bid - ep.tail_full, r = q / 8;
         piece = r % ep.tail_splits;
-        u = (r / ep.tail_splits) * 8 + q % 8;
+        // xcd_order: XCD q % 8 takes a contiguous run of tail tiles (a
+        // compact patch of C) instead of every 8th.
+        u = xcd_order ? (q % 8) * ((ep.tail_count + 7) / 8) + r / ep.tail_splits
+                      : (r / ep.tail_splits) * 8 + q % 8;
         if (u >= ep.tail_count) return -1;
         t = ep.tail_full + u;
     }
@@ -868,16 +872,18 @@ struct Tile {
 //   share (fc2 at M = 3460: 148 -> 140 us);
 // - long K (fc2 at 865 tokens, split K): 105 -> 50 MB fetched and written,
 //   time unchanged;
-// - 3072 columns and more (fc1 at 865 tokens): 43.8 -> 43.2 us;
-// and not for QKV and the out-projection at 865 tokens, which fetch less
-// with it but ran 0.3-0.4 us slower.  The convolution and patch-scatter
+// and not for the other launches at 865 tokens: QKV and the out-projection
+// fetch less with it but ran 0.3-0.4 us slower, and fc1's 48 column tiles
+// in launch order already give each XCD one strip of columns for its whole
+// and tail tiles alike (38 MB fetched against 44 MB with it, at the same
+// time).  The convolution and patch-scatter
 // GEMMs keep the row rule.  VESTRA_HIP_GEMM_XCD=0|1 forces it off or on (A/B
 // studies).
 int use_xcd_order(const GemmArgs &g) {
     static const char *env = std::getenv("VESTRA_HIP_GEMM_XCD");
     if (env && (env[0] == '0' || env[0] == '1') && env[1] == 0) return env[0] - '0';
     if (g.conv_in_c || g.scatter_kw) return g.m > 1024;
-    return g.m > 1024 || g.k >= 2048 || g.n >= 3072;
+    return g.m > 1024 || g.k >= 2048;
 }
 
 template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, int CONV = 0>
