@@ -218,6 +218,27 @@ def test_gemm_balanced_tail(rt, monkeypatch, m, k, n):
     assert (got.view(np.uint32) != whole.view(np.uint32)).any()
 
 
+@pytest.mark.parametrize("m", [865, 194])
+def test_fc2_tail_equals_split_k(rt, monkeypatch, m):
+    """A long-K projection whose 64 x 64 grid has fewer tiles than CUs (fc2:
+    K = 3072, N = 768; 168 and 48 tiles) runs as the balanced tail over the
+    split table's K ranges, so each output is the same sum of the same
+    partials as split-K 3 with its reduction kernel: bit for bit, residual
+    epilogue included."""
+    k, n = 3072, 768
+    a = rt.upload_f32(seeded.normal(61 + m, m * k))
+    ls = (0.1 + 0.9 * seeded.uniform01(64, n)).astype(np.float32)
+    lin = rt.prepare_linear_f32(k, n, seeded.normal(62, k * n, 0.02), seeded.normal(63, n, 0.02), ls)
+    x = seeded.normal(65, m * n)
+    xt = rt.upload_f32(x)
+    lin.run_residual(a, m, xt)
+    tail = rt.download_f32(xt)
+    monkeypatch.setenv("VESTRA_HIP_GEMM_TILE", "64x128x64x2x4x3")
+    xs = rt.upload_f32(x)
+    lin.run_residual(a, m, xs)
+    assert_bits_equal(tail, rt.download_f32(xs), "balanced tail against split-K 3")
+
+
 def test_gemm_balanced_tail_store_matches_float64(rt):
     """Store epilogue through the row-major GEMM: 336 tiles, K = 512 in two
     pieces; the fp32 error bound of test_gemm_row_major_matches_float64."""

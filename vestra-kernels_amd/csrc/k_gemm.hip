@@ -945,7 +945,9 @@ bool tile_override(Tile *t, int *splits) {
 // Per-shape defaults from the kernel-trace tile sweep on MI355X (DA3
 // projections at 865 and 4 x 865 tokens).  Only the long-K narrow projection
 // (fc2: K = 3072, N = 768) splits K: with K = 768 the 64x64 grid already
-// keeps every CU busy for less time than a separate reduction costs.
+// keeps every CU busy for less time than a separate reduction costs.  Where
+// the 64x64 grid of such a split launch has fewer tiles than CUs, dispatch
+// runs it as the balanced tail instead (K pieces summed by the last piece).
 void default_tile(const GemmArgs &g, Tile *t, int *splits) {
     *splits = 1;
     const bool narrow = g.n <= 1024;
@@ -996,8 +998,9 @@ struct TailPlan {
 // With fewer tiles than CUs there is no whole round and every tile runs as
 // pieces (the 865 x 768 x 768 projection: 168 tiles, 504 pieces).
 // VESTRA_HIP_GEMM_TAIL=0 turns the tail off and =1 takes it whenever it
-// lowers the load at all (A/B studies and tests).
-bool tail_plan(const GemmArgs &g, const Tile &t, TailPlan *plan) {
+// lowers the load at all (A/B studies and tests).  only_splits, if set, is
+// the one piece count allowed.
+bool tail_plan(const GemmArgs &g, const Tile &t, TailPlan *plan, int only_splits = 0) {
     if (t.bm != 64 || t.bn != 64 || t.bk != 32 || t.wm != 2 || t.wn != 2) return false;
     if (!g.tail_ws || !g.tail_cnt || g.k == 0 || g.k % 32 != 0) return false;
     const char *env = std::getenv("VESTRA_HIP_GEMM_TAIL");
@@ -1020,7 +1023,7 @@ bool tail_plan(const GemmArgs &g, const Tile &t, TailPlan *plan) {
     double best = forced ? whole : whole * 0.95;
     int pick = 0;
     for (int sp = 2; sp <= 4; sp++) {
-        if (ktiles % sp != 0 || ktiles / sp < 4) continue;
+        if (ktiles % sp != 0 || ktiles / sp < 4 || (only_splits && sp != only_splits)) continue;
         if ((size_t)count8 > g.tail_cnt_n || (size_t)(count8 * sp) * 64 * 64 > g.tail_ws_floats) continue;
         const double load = (double)(full / cus) + (double)((rem * sp + cus - 1) / cus) / sp;
         if (load < best) {
@@ -1056,14 +1059,27 @@ template <Epi EPI>
 hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     Tile t;
     int splits;
-    if (!tile_override(&t, &splits)) default_tile(g, &t, &splits);
+    const bool overridden = tile_override(&t, &splits);
+    if (!overridden) default_tile(g, &t, &splits);
     if (EPI == Epi::Qkv) splits = 1;
+    const int table_splits = !overridden && splits > 1 ? splits : 0;
     if (splits > 1 && (g.ws == nullptr || g.ws_floats < (size_t)splits * g.m * g.n)) splits = 1;
     if constexpr (EPI != Epi::Qkv) {
         // Store, GELU and Residual: the last piece of a tail tile runs the
         // epilogue once (a Residual tile adds its residual exactly once).
         TailPlan p;
         if (splits == 1 && tail_plan(g, t, &p)) return launch_tail<EPI>(s, g, ep, p);
+        // A long-K launch that the table splits, whose 64 x 64 grid has
+        // fewer tiles than CUs (fc2 at 865 tokens: 168 tiles): every tile as
+        // K pieces, the last piece of each summing them in order and running
+        // the epilogue, saves the separate reduction launch (fc2 41.3 against
+        // 42.1 us for split-K 3 of 64 x 128 tiles plus the reduction).  The
+        // pieces are the table's K ranges, so each output is the same sum of
+        // the same partials as split-K with its reduction (the encoder's
+        // fused fc2 reduction and LayerNorm still splits K that way).
+        if (table_splits && g.k % ((size_t)table_splits * t.bk) == 0 &&
+            tail_plan(g, Tile{64, 64, 32, 2, 2}, &p, table_splits) && p.full == 0)
+            return launch_tail<EPI>(s, g, ep, p);
     }
     if (splits == 1) {
         hipError_t e = run_cfg<EPI, false>(s, g, ep, t, 1);
