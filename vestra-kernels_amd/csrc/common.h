@@ -137,9 +137,11 @@ __device__ __forceinline__ f32x4 ln_apply(f32x4 x, float mean, float inv, f32x4 
 __device__ __forceinline__ float cephes_exp(float x) {
     x = (x < 88.37626f) ? x : 88.37626f;
     x = (x > -88.37626f) ? x : -88.37626f;
-    float fx0 = __fmaf_rn(x, 1.44269504f, 0.5f);
-    float tr = (float)(int)fx0;
-    float fx = (tr > fx0) ? sub_rn(tr, 1.0f) : tr;
+    // The reference truncates (cvttps) and subtracts one where truncation
+    // rose; after the clamps fx0 lies in [-127, 128], where that is floor
+    // (the same bits for all 2^32 inputs, checked on the host), one
+    // instruction instead of five.
+    const float fx = __builtin_floorf(__fmaf_rn(x, 1.44269504f, 0.5f));
     x = __fmaf_rn(-fx, 0.693359375f, x);
     x = __fmaf_rn(-fx, -2.1219444e-4f, x);
     float z = mul_rn(x, x);
