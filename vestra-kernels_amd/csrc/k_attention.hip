@@ -470,7 +470,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
+        __builtin_amdgcn_s_setprio(1);
         __builtin_amdgcn_sched_barrier(0);
+        // The softmax runs at raised wave priority: it is the chain between
+        // this wave's two contractions, and the SIMD's other wave keeps the
+        // matrix core busy meanwhile (attention at 865 tokens 31.7 -> 31.0
+        // us; priority over the QK MFMAs instead, or over the fragment reads
+        // as well, took 33.3 us).
         // Online softmax of query li over its 16 keys of the panel.  The max
         // is taken on the raw scores (the scale is positive) and the scale
         // is folded into the exponent's FMA; full panels need no mask.
@@ -513,6 +519,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int df = 0; df < 4; df++) o[df][r] *= cr;
         }
+        __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
         // O[q][4li + df] += P[q][key] V[key][4li + df], key = 16g + 4lh + st.
 #pragma unroll
