@@ -240,6 +240,13 @@ vh_status vh_quantize_q8_0_into(const vh_runtime *rt, const vh_tensor *x, size_t
  * block sums, f32 combine in block order.  Bit-exact. */
 vh_status vh_gemm_q8_0(const vh_runtime *rt, const vh_q8_tensor *a_q, const vh_q8_tensor *b_q,
                        size_t m, size_t n, size_t k, vh_tensor **out);
+/* Kernels::gemm_q8_0(m, n, k, a_q, b_q, c) (src/dispatch.rs:91-105) into a
+ * caller's [m, n] f32 tensor, as the reference writes c: VH_ERR_LENGTH_MISMATCH
+ * ("c.len() must be m * n", the reference's debug assertion,
+ * src/scalar.rs:37) unless c holds m * n floats.  Bit-exact, the same kernel
+ * as vh_gemm_q8_0. */
+vh_status vh_gemm_q8_0_into(const vh_runtime *rt, const vh_q8_tensor *a_q, const vh_q8_tensor *b_q,
+                            size_t m, size_t n, size_t k, vh_tensor *c);
 
 /* ---- Q8_0 projections -------------------------------------------------------- */
 /* A projection whose weights are GGUF-style BlockQ8_0 (src/lib.rs:33-38): the

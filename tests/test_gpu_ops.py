@@ -527,6 +527,30 @@ def test_gemm_q8_0_bit_exact(rt, m, n, k):
     assert_bits_equal(got, exp, "Q8_0 GEMM")
 
 
+def test_gemm_q8_0_into_an_existing_tensor(rt):
+    """Kernels::gemm_q8_0(m, n, k, a_q, b_q, c) writes the caller's c: equal
+    bit for bit to the allocating entry point and to the oracle, twice into
+    the same tensor (the second product overwrites every element, as a
+    NaN-filled c shows); a c of another length is the reference's length
+    assert (src/scalar.rs:37)."""
+    m, n, k = 865, 3072, 768
+    bq = O.quantize_rows_q8_0(seeded.normal(4802, n * k, 0.02), n, k)
+    b_dev = rt.q8_0_upload(bq, n, k)
+    c = rt.upload_f32(np.full(m * n, np.nan, np.float32))
+    for seed in (4803, 4804):
+        x = seeded.normal(seed, m * k)
+        a_dev = rt.quantize_q8_0(rt.upload_f32(x), m, k)
+        rt.gemm_q8_0_into(a_dev, b_dev, m, n, k, c)
+        got = rt.download_f32(c)
+        assert_bits_equal(got, rt.download_f32(rt.gemm_q8_0(a_dev, b_dev, m, n, k)), "into vs allocating")
+        exp = O.gemm_q8_0(O.quantize_rows_q8_0(x, m, k), bq, m, n, k, impl="kernels")
+        assert_bits_equal(got, exp, "into vs oracle")
+    with pytest.raises(vh.LengthMismatch):
+        rt.gemm_q8_0_into(a_dev, b_dev, m, n, k, rt.upload_f32(np.zeros(m * n - 1, np.float32)))
+    with pytest.raises(vh.LengthMismatch):
+        rt.gemm_q8_0_into(a_dev, b_dev, m - 1, n, k, c)
+
+
 def test_flash_key_layouts_deterministic_and_consistent(rt, monkeypatch):
     """Every key layout -- one key stream per workgroup (direct-to-LDS panels,
     or register-staged panels with DIRECT=0), two streams per workgroup

@@ -1709,6 +1709,32 @@ extern "C" vh_status vh_gemm_q8_0(const vh_runtime *rt, const vh_q8_tensor *a_q,
     GUARD_END
 }
 
+extern "C" vh_status vh_gemm_q8_0_into(const vh_runtime *rt, const vh_q8_tensor *a_q,
+                                       const vh_q8_tensor *b_q, size_t m, size_t n, size_t k,
+                                       vh_tensor *c) {
+    NEED(rt, "vh_gemm_q8_0_into");
+    NEED(a_q, "vh_gemm_q8_0_into");
+    NEED(b_q, "vh_gemm_q8_0_into");
+    NEED(c, "vh_gemm_q8_0_into");
+    if (k % 32 != 0)
+        return fail(VH_ERR_KERNEL, "k must be a multiple of QK8_0, got " + std::to_string(k));
+    if (a_q->rows != m || a_q->k != k || b_q->rows != n || b_q->k != k)
+        return mismatch(a_q->rows * a_q->k, m * k, "vh_gemm_q8_0_into operand shape");
+    size_t mn = 0;
+    if (mul_overflows(m, n, &mn) || c->len != mn) return mismatch(c->len, mn, "c.len() must be m * n");
+    if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
+        return fail(VH_ERR_KERNEL, "vh_gemm_q8_0_into dimension exceeds 2^31-1");
+    if (c->rt != rt->s || a_q->rt != rt->s || b_q->rt != rt->s)
+        return fail(VH_ERR_KERNEL, "vh_gemm_q8_0_into: a tensor belongs to another runtime");
+    GUARD_BEGIN
+    RtState &s = *rt->s;
+    TRY(set_device(s));
+    return launch(s, "gemm_q8_0", [&] {
+        return vh::launch_gemm_q8_0(s.stream, a_q->qs, a_q->d, b_q->qs, b_q->d, c->ptr, m, n, k);
+    });
+    GUARD_END
+}
+
 // ---- Q8_0 projection --------------------------------------------------------
 
 extern "C" vh_status vh_prepare_linear_q8_0(const vh_runtime *rt, size_t input_features,

@@ -189,6 +189,8 @@ unsafe extern "C" {
                              out: *mut VhQ8Tensor) -> Status;
     fn vh_gemm_q8_0(rt: *const VhRuntime, a_q: *const VhQ8Tensor, b_q: *const VhQ8Tensor, m: usize, n: usize,
                     k: usize, out: *mut *mut VhTensor) -> Status;
+    fn vh_gemm_q8_0_into(rt: *const VhRuntime, a_q: *const VhQ8Tensor, b_q: *const VhQ8Tensor, m: usize,
+                         n: usize, k: usize, c: *mut VhTensor) -> Status;
 
     fn vh_prepare_linear_q8_0(rt: *const VhRuntime, input_features: usize, output_features: usize,
                               weight_blocks: *const c_void, bias: *const f32, gamma: *const f32,
@@ -710,6 +712,16 @@ impl HipRuntime {
         let raw = self.inner.raw;
         // SAFETY: live handles.
         self.make(|out| unsafe { vh_gemm_q8_0(raw, a_q.raw, b_q.raw, m, n, k, out) })
+    }
+
+    /// Kernels::gemm_q8_0(m, n, k, a_q, b_q, c) into an existing [m, n]
+    /// tensor of this runtime, as the reference writes `c`.
+    pub fn gemm_q8_0_into(&self, a_q: &HipQ8Tensor, b_q: &HipQ8Tensor, m: usize, n: usize, k: usize,
+                          c: &mut HipTensorF32) -> Result<(), HipError> {
+        let raw = self.inner.raw;
+        let dst = c.raw;
+        // SAFETY: live handles; `c` is borrowed mutably for the call.
+        self.call(|| unsafe { vh_gemm_q8_0_into(raw, a_q.raw, b_q.raw, m, n, k, dst) })
     }
 
     /// A projection with BlockQ8_0 weights (rows of W^T), bias and gamma [N].

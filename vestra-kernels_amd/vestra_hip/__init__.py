@@ -131,6 +131,7 @@ SIGNATURES = [
     ("vh_quantize_q8_0", _S, [_p, _p, _sz, _sz, _pp]),
     ("vh_quantize_q8_0_into", _S, [_p, _p, _sz, _sz, _p]),
     ("vh_gemm_q8_0", _S, [_p, _p, _p, _sz, _sz, _sz, _pp]),
+    ("vh_gemm_q8_0_into", _S, [_p, _p, _p, _sz, _sz, _sz, _p]),
     ("vh_prepare_linear_q8_0", _S, [_p, _sz, _sz, _p, _f32p, _f32p, _pp]),
     ("vh_linear_q8_0_free", None, [_p]),
     ("vh_linear_q8_0_input_features", _sz, [_p]),
@@ -614,6 +615,10 @@ class Runtime:
 
     def gemm_q8_0(self, a_q: Q8Tensor, b_q: Q8Tensor, m, n, k) -> Tensor:
         return self._out(lib().vh_gemm_q8_0, a_q.handle, b_q.handle, m, n, k)
+
+    def gemm_q8_0_into(self, a_q: Q8Tensor, b_q: Q8Tensor, m, n, k, c: Tensor) -> None:
+        """Kernels::gemm_q8_0 into an existing [m, n] tensor (the reference's c)."""
+        _check(lib().vh_gemm_q8_0_into(self._h, a_q.handle, b_q.handle, m, n, k, c.handle))
 
     def prepare_linear_q8_0(self, input_features, output_features, weight_blocks, bias=None,
                             gamma=None) -> LinearQ8:
