@@ -69,6 +69,22 @@ __device__ __forceinline__ float div_rn(float a, float b) {
 // 53 >= 2*24 + 2 makes double rounding innocuous for sqrt.
 __device__ __forceinline__ float sqrt_rn(float x) { return (float)__builtin_sqrt((double)x); }
 
+// p[i] when p is non-null, else `fallback`, with the load itself
+// unconditional: it reads alt[i] (any valid address) when p is null, and the
+// value is selected afterwards.  A load inside a branch leaves the compiler's
+// wait insertion unsure at the join whether it is still pending, and it then
+// waits for every load and store in flight there.
+template <class T>
+__device__ __forceinline__ T load_or(const T *p, const T *alt, size_t i, T fallback) {
+    const T v = (p ? p : alt)[i];
+    return p ? v : fallback;
+}
+
+// s_waitcnt vmcnt(0): every vector memory load and store of the wave done.
+// Placed after a group of epilogue reads, it leaves nothing pending, so the
+// stores that follow need no waits between them (vmcnt counts stores too).
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
 // One DPP lane permutation (a VALU modifier, no LDS round trip).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {

@@ -556,6 +556,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
         for (int i = 0; i < FM; i++)
 #pragma unroll
             for (int r = 0; r < 4; r++) bias[i][r] = ep.bias ? ep.bias[min(rbase + i * 16 + r, M - 1)] : 0.0f;
+        wait_vmem_all();  // then the guarded stores need no waits between them
 #pragma unroll
         for (int j = 0; j < FN; j++) {
             const int n = cbase + j * 16;
@@ -590,6 +591,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
         for (int i = 0; i < FM; i++)
 #pragma unroll
             for (int r = 0; r < 4; r++) bias[i][r] = ep.bias ? ep.bias[min(rbase + i * 16 + r, M - 1)] : 0.0f;
+        wait_vmem_all();  // then the guarded stores need no waits between them
         const int cbase = n0 + wn * TN + li;
 #pragma unroll
         for (int j = 0; j < FN; j++) {
@@ -640,6 +642,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                     }
                 }
         }
+        wait_vmem_all();  // then the guarded stores need no waits between them
 #pragma unroll
         for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -675,8 +678,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
 #pragma unroll
         for (int j = 0; j < FN; j++) {
             const int col = min(cbase + j * 16, N - 1);
-            bias[j] = ep.bias ? ep.bias[col] : 0.0f;
-            gamma[j] = ep.gamma ? ep.gamma[col] : 1.0f;
+            bias[j] = load_or(ep.bias, (const float *)ep.c, col, 0.0f);
+            gamma[j] = load_or(ep.gamma, (const float *)ep.c, col, 1.0f);
         }
         float resid[EPI == Epi::Residual ? FM : 1][FN][4];
         if constexpr (EPI == Epi::Residual) {
@@ -690,6 +693,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                         resid[i][j][r] = ep.c[row * N + min(cbase + j * 16, N - 1)];
                     }
         }
+        wait_vmem_all();  // then the guarded stores need no waits between them
         // A tile wholly inside C and, for GELU, wholly before the scalar
         // tail (the last n % 16 values, tail_start on) stores without
         // per-element checks; the decision is per tile, so the branch is
@@ -776,8 +780,8 @@ __global__ __launch_bounds__(256) void splitk_reduce4_kernel(int M, int N, EpiAr
     f32x4 p[SPLITS];
 #pragma unroll
     for (int sp = 0; sp < SPLITS; sp++) p[sp] = part[(size_t)sp * mn4 + i4];
-    const f32x4 b = ep.bias ? *reinterpret_cast<const f32x4 *>(ep.bias + col) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const f32x4 g = ep.gamma ? *reinterpret_cast<const f32x4 *>(ep.gamma + col) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+    const f32x4 b = load_or(reinterpret_cast<const f32x4 *>(ep.bias), part, col / 4, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+    const f32x4 g = load_or(reinterpret_cast<const f32x4 *>(ep.gamma), part, col / 4, f32x4{1.0f, 1.0f, 1.0f, 1.0f});
     f32x4 *c4 = reinterpret_cast<f32x4 *>(ep.c) + i4;
     f32x4 x = EPI == Epi::Residual ? *c4 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 v = p[0];
@@ -821,7 +825,7 @@ __global__ __launch_bounds__(256) void splitk_residual_ln_kernel(int M, int N, E
     f32x4 *c4 = reinterpret_cast<f32x4 *>(ep.c + (size_t)row * N);
     const f32x4 *bias4 = reinterpret_cast<const f32x4 *>(ep.bias);
     const f32x4 *gamma4 = reinterpret_cast<const f32x4 *>(ep.gamma);
-    f32x4 p[4][SPLITS], x[4], b[4], g[4];
+    f32x4 p[4][SPLITS], x[4], b[4], g[4], lg[4], lb[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int idx = lane + j * 64 < n4 ? lane + j * 64 : 0;
@@ -829,9 +833,12 @@ __global__ __launch_bounds__(256) void splitk_residual_ln_kernel(int M, int N, E
 #pragma unroll
         for (int sp = 0; sp < SPLITS; sp++) p[j][sp] = part[(size_t)sp * mn4 + i4];
         x[j] = c4[idx];
-        b[j] = ep.bias ? bias4[idx] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        g[j] = ep.gamma ? gamma4[idx] : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+        b[j] = load_or(bias4, (const f32x4 *)c4, idx, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        g[j] = load_or(gamma4, (const f32x4 *)c4, idx, f32x4{1.0f, 1.0f, 1.0f, 1.0f});
+        lg[j] = reinterpret_cast<const f32x4 *>(ln_g)[idx];
+        lb[j] = reinterpret_cast<const f32x4 *>(ln_b)[idx];
     }
+    wait_vmem_all();  // one wait for all of them; the stores below then need none
     f32x4 r[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -856,9 +863,7 @@ __global__ __launch_bounds__(256) void splitk_residual_ln_kernel(int M, int N, E
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int idx = lane + j * 64;
-        if (idx < n4)
-            y4[idx] = ln_apply(r[j], mean, inv, reinterpret_cast<const f32x4 *>(ln_g)[idx],
-                               reinterpret_cast<const f32x4 *>(ln_b)[idx]);
+        if (idx < n4) y4[idx] = ln_apply(r[j], mean, inv, lg[j], lb[j]);
     }
 }
 

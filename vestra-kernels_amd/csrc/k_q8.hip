@@ -297,43 +297,66 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
     // LDS as floats at the chunk's start.  Chunk 0's loads go out before
     // the operand prefetch, so that the first wait for them leaves the
     // prefetch in flight.
+    // Thread tid stages element e = tid + 256 t of the chunk: block e / TR
+    // (clamped to the last block), row m0 + e % TR (clamped).  As TR divides
+    // 64, e % TR is lane % TR, a loop-invariant lane offset.  With 64-row
+    // (64-column) tiles the block e / TR = wave + 4 t is uniform per wave: a
+    // buffer load then takes it as an SGPR offset, with no vector address
+    // arithmetic; 32-row tiles form the offset in 32-bit lane arithmetic.
+    // Blocks past the chunk fill LDS rows that are never read.
     constexpr int NA = TR * QCH / 256, NB = TC * QCH / 256;
+    static_assert(64 % TR == 0 && 64 % TC == 0, "staging layout");
+    const __amdgpu_buffer_rsrc_t rsda =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a_d, (short)0, nb * M * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsdb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)b_d, (short)0, nb * N * 2, 0x00020000);
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int rowa = min(m0 + lane % TR, M - 1), colb = min(n0 + lane % TC, N - 1);
     uint16_t ra[NA], rb[NB];
     auto load_scales = [&](int c) {
-        const int last = min(QCH, nb - c) - 1;
 #pragma unroll
         for (int t = 0; t < NA; t++) {
-            const int e = tid + 256 * t, blk = min(e / TR, last);
-            ra[t] = a_d[(size_t)(c + blk) * M + min(m0 + e % TR, M - 1)];
+            if constexpr (TR == 64) {
+                const int blk = min(c + wv + 4 * t, nb - 1);
+                ra[t] = __builtin_amdgcn_raw_buffer_load_b16(rsda, rowa * 2, blk * M * 2, 0);
+            } else {
+                const int blk = min(c + (tid + 256 * t) / TR, nb - 1);
+                ra[t] = __builtin_amdgcn_raw_buffer_load_b16(rsda, (blk * M + rowa) * 2, 0, 0);
+            }
         }
 #pragma unroll
         for (int t = 0; t < NB; t++) {
-            const int e = tid + 256 * t, blk = min(e / TC, last);
-            rb[t] = b_d[(size_t)(c + blk) * N + min(n0 + e % TC, N - 1)];
+            if constexpr (TC == 64) {
+                const int blk = min(c + wv + 4 * t, nb - 1);
+                rb[t] = __builtin_amdgcn_raw_buffer_load_b16(rsdb, colb * 2, blk * N * 2, 0);
+            } else {
+                const int blk = min(c + (tid + 256 * t) / TC, nb - 1);
+                rb[t] = __builtin_amdgcn_raw_buffer_load_b16(rsdb, (blk * N + colb) * 2, 0, 0);
+            }
         }
     };
-    auto store_scales = [&](int cn) {
+    auto store_scales = [&]() {
 #pragma unroll
-        for (int t = 0; t < NA; t++) {
-            const int e = tid + 256 * t;
-            if (e / TR < cn) sa[e / TR][e % TR] = half_bits_to_float(ra[t]);
-        }
+        for (int t = 0; t < NA; t++) (&sa[0][0])[tid + 256 * t] = half_bits_to_float(ra[t]);
 #pragma unroll
-        for (int t = 0; t < NB; t++) {
-            const int e = tid + 256 * t;
-            if (e / TC < cn) sb[e / TC][e % TC] = half_bits_to_float(rb[t]);
-        }
+        for (int t = 0; t < NB; t++) (&sb[0][0])[tid + 256 * t] = half_bits_to_float(rb[t]);
     };
     i32x4 cur[FM][FN];
     if (nb > 0) {  // K == 0 stores zeros
         load_scales(0);
+        // Slot by slot, in the loop's order, so that the loop's first waits
+        // need only their own slot's loads.
 #pragma unroll
-        for (int p = 0; p < QPF; p++) fetch(p, p);
+        for (int p = 0; p < QPF; p++) {
+            fetch(p, p);
+            __builtin_amdgcn_sched_barrier(0x0006);
+        }
         block_sums(0, cur);
         fetch(QPF, 0);
+        __builtin_amdgcn_sched_barrier(0x0006);
         // Chunk 0's scales, outside the chunk loop so that their wait
         // leaves the operand prefetch in flight.
-        store_scales(min(QCH, nb));
+        store_scales();
     }
 
     for (int c0 = 0; c0 < nb; c0 += QCH) {
@@ -341,7 +364,7 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
         if (c0 > 0) {
             __syncthreads();  // the previous chunk's scales are no longer read
             load_scales(c0);
-            store_scales(cn);
+            store_scales();
         }
         __syncthreads();
         // Groups of QPF blocks with the prefetch slots fixed at compile time
@@ -370,6 +393,11 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
                 i32x4 nxt[FM][FN];
                 block_sums((u + 1) % QPF, nxt);
                 fetch(b + 1 + QPF, (u + 1) % QPF);
+                // Keep each block's MFMAs and the loads that refill its slot
+                // in this order (only VALU and SALU work may move across):
+                // hoisting the next block's MFMAs above these loads makes
+                // the loop wait for every load in flight.
+                __builtin_amdgcn_sched_barrier(0x0006);
                 f32x4 da_n[FM];
                 float db_n[FN];
                 read_scales(min(bl + u + 1, cn - 1), da_n, db_n);
@@ -401,6 +429,14 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
         bias[j] = ep.bias ? ep.bias[col] : 0.0f;
         gamma[j] = ep.gamma ? ep.gamma[col] : 1.0f;
     }
+    // A whole tile (and, for GELU, wholly below tail_start) addresses its
+    // elements as a wave-uniform row pointer plus one 32-bit lane offset,
+    // with no bounds checks: no vector address arithmetic per element.
+    const int mwu = m0 + (wv >> 1) * 16 * FM, nwu = n0 + (wv & 1) * 16 * FN;  // mw, nw
+    const bool whole = m0 + TR <= M && n0 + TC <= N &&
+                       (EPI != Epi::Gelu || (size_t)(m0 + TR - 1) * N + n0 + TC <= ep.tail_start);
+    const unsigned loff = (unsigned)(4 * lh * N + li);
+    auto row_ptr = [&](int i, int j, int r) { return c + (size_t)(mwu + i * 16 + r) * N + nwu + j * 16; };
     if constexpr (EPI == Epi::Residual) {
 #pragma unroll
         for (int i = 0; i < FM; i++)
@@ -408,9 +444,16 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
             for (int j = 0; j < FN; j++)
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    resid[i][j][r] = c[(size_t)min(mw + i * 16 + 4 * lh + r, M - 1) * N +
-                                       min(nw + j * 16 + li, N - 1)];
+                    resid[i][j][r] = whole ? row_ptr(i, j, r)[loff]
+                                           : c[(size_t)min(mw + i * 16 + 4 * lh + r, M - 1) * N +
+                                               min(nw + j * 16 + li, N - 1)];
     }
+    // One wait for every load in flight (these reads and the loop's last,
+    // unused prefetch) before the stores.  Without it the optional bias and
+    // gamma loads leave a possibly pending load at every join of the guarded
+    // stores below, and as vmcnt counts stores too, each store then waited
+    // for the one before it (about 2.4 us for a tile's 16 stores).
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     if constexpr (EPI == Epi::Gelu && FN == 2) {
         if (ep.q8_qs) {
             // A row's 32-column block nw .. nw + 31 is fragments j = 0, 1 of
@@ -499,6 +542,25 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
                 orow[li] = a;
                 orow[16 + li] = b;
             }
+        return;
+    }
+    if (whole) {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float v = acc[i][j][r];
+                    if (ep.bias) v = add_rn(v, bias[j]);
+                    if constexpr (EPI == Epi::Gelu) {
+                        v = gelu_avx512_form(v);
+                    } else {
+                        if (ep.gamma) v = mul_rn(v, gamma[j]);
+                        if constexpr (EPI == Epi::Residual) v = add_rn(resid[i][j][r], v);
+                    }
+                    row_ptr(i, j, r)[loff] = v;
+                }
         return;
     }
 #pragma unroll
