@@ -674,7 +674,7 @@ def main() -> int:
                     help="also run 5 residual-add kernels over 16M floats (reads 128 MiB, "
                          "writes 64 MiB each) to scale PMC byte counters")
     ap.add_argument("--only", choices=["q8_0", "elementwise", "dpt", "encoder", "configs", "block",
-                                       "block4"],
+                                       "block4", "q8_0_block"],
                     help="run one secondary section alone and print its JSON (for profiling "
                          "runs; not the benchmark line)")
     args = ap.parse_args()
@@ -689,7 +689,8 @@ def main() -> int:
                    "elementwise": gpu_elementwise, "dpt": gpu_dpt,
                    "encoder": gpu_encoder, "configs": gpu_configs,
                    "block": lambda: BlockBench().steady(args.steps),
-                   "block4": lambda: BlockBench(images=4).steady(args.steps)}[args.only]
+                   "block4": lambda: BlockBench(images=4).steady(args.steps),
+                   "q8_0_block": lambda: BlockBench(q8_0=True).steady(args.steps)}[args.only]
         print(json.dumps({args.only: section()}), flush=True)
         return 0
 
