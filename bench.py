@@ -50,7 +50,7 @@ T = 865
 D, H, HD, F = 768, 12, 64, 3072
 FLOPS = {
     "gemm_qkv_rope": 2.0 * T * D * 3 * D,
-    "gemm_proj_residual_ln": 2.0 * T * D * D,
+    "gemm_proj_residual": 2.0 * T * D * D,
     "gemm_fc1_gelu": 2.0 * T * D * F,
     "gemm_fc2_residual": 2.0 * T * F * D,
     "flash_attention": 4.0 * H * T * T * HD,
@@ -462,7 +462,7 @@ def gpu_dpt(reps: int = 20) -> dict:
 
 
 # BASELINE config 2 shapes (K, N) per launch, and the config-1 attention.
-PROJ_SHAPES = {"gemm_qkv_rope": (D, 3 * D), "gemm_proj_residual_ln": (D, D),
+PROJ_SHAPES = {"gemm_qkv_rope": (D, 3 * D), "gemm_proj_residual": (D, D),
                "gemm_fc1_gelu": (D, F), "gemm_fc2_residual": (F, D)}
 
 
@@ -568,9 +568,9 @@ def cpu_kernels() -> dict:
     q, k, v = config1_qkv()
     work = {
         "gemm_qkv_rope": lambda: oracle.qkv(*ins["gemm_qkv_rope"], T),
-        "gemm_proj_residual_ln": lambda: oracle.linear_bias_scale(
-            ins["gemm_proj_residual_ln"][0], ins["gemm_proj_residual_ln"][1],
-            ins["gemm_proj_residual_ln"][2], ones[:D], T, D, D),
+        "gemm_proj_residual": lambda: oracle.linear_bias_scale(
+            ins["gemm_proj_residual"][0], ins["gemm_proj_residual"][1],
+            ins["gemm_proj_residual"][2], ones[:D], T, D, D),
         "gemm_fc1_gelu": lambda: oracle.linear(ins["gemm_fc1_gelu"][0], ins["gemm_fc1_gelu"][1],
                                                T, F, D),
         "gemm_fc2_residual": lambda: oracle.linear_bias_scale(
@@ -579,7 +579,7 @@ def cpu_kernels() -> dict:
         "flash_attention": lambda: oracle.flash_attention_avx512(q, k, v, H, T),
     }
     names = {"gemm_qkv_rope": "qkv_f32_da3_base 865x768x2304",
-             "gemm_proj_residual_ln": "linear_bias_scale_f32_da3_base 865x768x768",
+             "gemm_proj_residual": "linear_bias_scale_f32_da3_base 865x768x768",
              "gemm_fc1_gelu": "linear_f32_da3_base 865x768x3072",
              "gemm_fc2_residual": "linear_bias_scale_f32_da3_base 865x3072x768",
              "flash_attention": "flash_attention_f32_da3_base 12x865x64"}

@@ -70,6 +70,47 @@ def test_block_batch_images_match_single_image_runs(rt):
     assert max_rel(rt.download_f32(single), got[T * 768:2 * T * 768]) <= 1e-5
 
 
+@pytest.mark.parametrize("stats", ["producer", "slices"])
+@pytest.mark.parametrize("images, qk_norm", [(1, False), (4, False), (1, True)],
+                         ids=["865", "4x865", "late_865"])
+def test_block_layernorm_affine_and_row_offsets(rt, monkeypatch, images, qk_norm, stats):
+    """The f32 block folds LayerNorm 1 and 2 into the QKV and fc1 GEMMs
+    (gamma into the weight, beta into the bias, the row mean and 1/std
+    applied in the epilogue).  The row statistics come from the
+    out-projection's per-chunk statistics (fc1; "producer") or from the GEMM's
+    own A slices (QKV of a lone block, and fc1 with VESTRA_HIP_LN_STATS=0;
+    "slices").  Per-channel LayerNorm gamma ~ U(0.5, 1.5) and beta ~
+    N(0, 0.1^2), and input rows with their own offset (N(0, 3^2)) and scale
+    (U(0.5, 2)), check the fold against the oracle's LayerNorm -> linear; a
+    block whose LayerNorms dropped gamma and beta misses the bar by 10x
+    (control computed with the oracle)."""
+    if stats == "slices":
+        monkeypatch.setenv("VESTRA_HIP_LN_STATS", "0")
+    T = 865
+    w = da3.block_weights(seed=11, layerscale="uniform", ln_affine=True, qk_norm=qk_norm)
+    z = seeded.normal(1100 + images, images * T * 768).reshape(-1, 768)
+    rows = z.shape[0]
+    off = seeded.normal(1200, rows, 3.0)[:, None]
+    scale = (0.5 + 1.5 * seeded.uniform01(1300, rows))[:, None]
+    x = (off + scale * z).astype(np.float32).reshape(-1)
+    pos = da3.positions_yx(24, 36)
+    exp = O.vit_block(x, w, images, T, pos)
+    blk = rt.prepare_block(w)
+    xt = rt.upload_f32(x)
+    rt.vit_block_run(blk, xt, images, T, pos)
+    got = rt.download_f32(xt)
+    assert np.isfinite(got).all()
+    assert max_rel(got, exp) <= BLOCK_TOL
+    assert max_rel(_branch(got, x), _branch(exp, x)) <= BLOCK_TOL * 10
+    plain = dict(w)
+    for key in ("ln1_gamma", "ln2_gamma"):
+        plain[key] = np.ones(768, np.float32)
+    for key in ("ln1_beta", "ln2_beta"):
+        plain[key] = np.zeros(768, np.float32)
+    wrong = O.vit_block(x, plain, images, T, pos)
+    assert max_rel(_branch(wrong, x), _branch(exp, x)) >= 100 * BLOCK_TOL
+
+
 def test_block_no_rope_and_odd_tokens(rt):
     T = 97
     w = da3.block_weights(seed=5, layerscale=1.0)
@@ -142,10 +183,12 @@ def test_encoder_config5a_da3_layerscale(rt):
 
 @pytest.mark.parametrize("images, T", [(1, 865), (2, 97)])
 def test_encoder_fused_norms_match_block_by_block_runs(rt, images, T):
-    """Inside the encoder each fc2 reduction also writes the next layer's
-    LayerNorm1 input; block by block, a separate LayerNorm kernel does.  Both
-    round every element the same way, so three layers agree bit for bit."""
-    ws = [da3.block_weights(seed=9, layer=l, layerscale=0.5) for l in range(3)]
+    """Inside the encoder each fc2 also writes the row statistics of its
+    output, from which the next layer's QKV takes its LayerNorm; block by
+    block, the QKV takes them from its own A slices.  Both are the same
+    statistics up to rounding: three layers agree to 1e-5, and both match
+    the oracle."""
+    ws = [da3.block_weights(seed=9, layer=l, layerscale=0.5, ln_affine=True) for l in range(3)]
     x = seeded.normal(900 + T, images * T * 768)
     pos = da3.positions_yx(24, 36) if T == 865 else None
     blocks = [rt.prepare_block(w) for w in ws]
@@ -156,7 +199,10 @@ def test_encoder_fused_norms_match_block_by_block_runs(rt, images, T):
         rt.vit_block_run(b, step, images, T, pos)
     a, b = rt.download_f32(fused), rt.download_f32(step)
     assert np.isfinite(a).all()
-    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert max_rel(_branch(a, x), _branch(b, x)) <= 1e-5
+    exp = O.encoder(x, ws, images, T, pos)
+    assert max_rel(a, exp) <= ENCODER_TOL
+    assert max_rel(_branch(a, x), _branch(exp, x)) <= BLOCK_TOL * 10
 
 
 @pytest.mark.parametrize("layout, T", [("local", 865), ("global", 865), ("none", 97)])
@@ -179,8 +225,9 @@ def test_late_block_qk_norm_vs_oracle(rt, layout, T):
 
 def test_encoder_with_late_blocks_vs_oracle(rt):
     """Four layers, the last two DA3 late blocks (Q/K LayerNorm), 2 images,
-    per-channel LayerScale in U(0.1, 1); the fused run equals block-by-block
-    runs bit for bit."""
+    per-channel LayerScale in U(0.1, 1); the encoder run (row statistics
+    passed from each fc2 to the next QKV) matches block-by-block runs (each
+    QKV taking them from its A slices) to 1e-5."""
     T, layers, images = 865, 4, 2
     ws = [da3.block_weights(seed=23, layer=l, qk_norm=l >= 2, layerscale="uniform")
           for l in range(layers)]
@@ -196,7 +243,7 @@ def test_encoder_with_late_blocks_vs_oracle(rt):
     step = rt.upload_f32(x)
     for b in blocks:
         rt.vit_block_run(b, step, images, T, pos)
-    assert np.array_equal(got.view(np.uint32), rt.download_f32(step).view(np.uint32))
+    assert max_rel(_branch(got, x), _branch(rt.download_f32(step), x)) <= 1e-5
 
 
 def test_late_block_needs_all_four_qk_norm_vectors(rt):

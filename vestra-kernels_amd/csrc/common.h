@@ -107,6 +107,19 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Sum over each aligned group of G consecutive lanes (G = 2, 4, 8 or 16):
+// the first log2(G) DPP steps of wave_sum; every lane of a group ends with
+// the group's total.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(G == 2 || G == 4 || G == 8 || G == 16, "DPP lane groups within a row");
+    v += dpp_f32<0xb1>(v);
+    if constexpr (G >= 4) v += dpp_f32<0x4e>(v);
+    if constexpr (G >= 8) v += dpp_f32<0x141>(v);
+    if constexpr (G >= 16) v += dpp_f32<0x140>(v);
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

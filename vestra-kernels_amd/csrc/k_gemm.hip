@@ -26,6 +26,18 @@
 //   Gelu     : c = gelu(acc + bias)              (fc1, Kernels::gelu forms)
 //   Residual : c = c + (acc + bias) * gamma      (out-proj / fc2 + residual)
 //   Qkv      : head-major Q/K/V with bias and the 2-D RoPE rotation of Q, K
+//
+// LayerNorm fold (LNF, Gelu and Qkv): the GEMM of a pre-norm sub-layer,
+// LayerNorm(x) . W^T + b with LayerNorm gamma g and beta be, is computed as
+//     rstd * (x . W'^T - mean * c) + b',   W' = W diag(g),
+//     c[n] = sum_k W'[n][k],               b' = b + W . be,
+// on the raw rows x (W', c and b' prepared once).  Every workgroup sees
+// whole rows of A (K is not split), so the row statistics come from the A
+// slices as they pass through registers on their way to LDS: each thread
+// sums (x - s) and (x - s)^2 over its chunks, with s = x[row][0] as a shift
+// that keeps the variance free of cancellation, and the threads of a row
+// reduce once after the slice loop.  Balanced-tail pieces publish their
+// sums beside their partial tiles; the last piece adds them in piece order.
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
@@ -69,6 +81,17 @@ struct EpiArgs {
     // between launches (the last piece resets it).
     int tail_full, tail_splits, tail_count, tail_kps;
     unsigned *tail_cnt;
+    // LayerNorm fold (LNF kernels): per-row sums of the tail pieces
+    // ([tail tile][piece][2 * ACH][threads]), c[n] = sum_k Bt[n][k] and eps.
+    float *tail_stats;
+    const float *ln_c;
+    float ln_eps;
+    // Row statistics per 32-column chunk, (mean, M2) pairs [M][stats_chunks]:
+    // written by a Residual epilogue (stats_out, wave tiles 32 columns wide)
+    // for the next pre-norm GEMM, read by LNF == 2 kernels (stats_in).
+    float2 *stats_out;
+    const float2 *stats_in;
+    int stats_chunks;
 };
 
 // Applies a Store / Gelu / Residual epilogue to one output element.
@@ -187,7 +210,7 @@ constexpr size_t gemm_lds_bytes() {
 // zeroed when the slice is stored to LDS (after the MFMAs), and the output
 // is the channel-major tile itself, i.e. CHW.
 template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, int CONV = 0,
-          bool TAIL = false>
+          bool TAIL = false, int LNF = 0>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__restrict__ A,
                                                               const float *__restrict__ Bt,
                                                               int M, int N, int K,
@@ -248,8 +271,16 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
         cd_x = x * ep.cd_stride - ep.cd_pad;
     }
 
-    f32x4 ra[ACH], rb[BCH];
-    auto gload = [&](int k0) {
+    // A registers of the slice in flight.  LNF keeps two sets, by slice
+    // parity, so that the LayerNorm sums of a slice read registers that no
+    // load is writing (and need no wait of their own); otherwise one set.
+    constexpr bool LN_LOOP = LNF == 1;  // row sums taken from the A slices
+    constexpr bool LN_ANY = LNF != 0;
+    f32x4 ra_sets[LN_LOOP ? 2 : 1][ACH], rb[BCH];
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    auto gload = [&](int k0, auto par) {
+        f32x4 *ra = ra_sets[LN_LOOP ? decltype(par)::value : 0];
         if constexpr (EXACT) {
 #pragma unroll
             for (int i = 0; i < ACH; i++) {
@@ -319,7 +350,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
             }
         }
     };
-    auto lstore = [&](int buf) {
+    auto lstore = [&](int buf, auto par) {
+        const f32x4 *ra = ra_sets[LN_LOOP ? decltype(par)::value : 0];
         float *as = smem + buf * STAGE;
         float *bs = as + BM * BK;
 #pragma unroll
@@ -346,6 +378,53 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                 int c = tid + i * NT;
                 *reinterpret_cast<f32x4 *>(&bs[swz<BK>(c / CPR, c % CPR)]) = rb[i];
             }
+        }
+    };
+
+    // LayerNorm fold: this thread's A chunks c = tid + i * NT all lie in row
+    // c / CPR of the tile (NT is a multiple of CPR); ln_sh[i] is that row's
+    // first element, ln_s1 / ln_s2 the shifted sums over the chunks seen.
+    constexpr int LA = LN_LOOP ? ACH : 1;
+    float ln_sh[LA], ln_s1[LA], ln_s2[LA];
+    if constexpr (LN_ANY)
+        static_assert(EXACT && !SPLIT && CONV == 0 && (EPI == Epi::Gelu || EPI == Epi::Qkv),
+                      "LayerNorm fold: whole-slice Gelu / Qkv GEMMs");
+    if constexpr (LN_LOOP) {
+        static_assert(NT % CPR == 0, "a thread's chunks share one row");
+#pragma unroll
+        for (int i = 0; i < ACH; i++) {
+            ln_sh[i] = A[(size_t)min(m0 + (tid + i * NT) / CPR, M - 1) * K];
+            ln_s1[i] = 0.0f;
+            ln_s2[i] = 0.0f;
+        }
+    }
+    // LNF == 2: the producer's statistics of this tile's rows, one (mean,
+    // M2) per 32-column chunk of the row (stats_chunks per row), prefetched
+    // before the slice loop: TPR threads per row, ln_cpt chunks each (host:
+    // stats_chunks == ln_cpt * TPR, ln_cpt <= LCP).  The loads are clamped,
+    // not selected, so that nothing waits for them before the loop.
+    constexpr int TPR = NT / BM, LCP = 8;
+    float2 ln_ch[LNF == 2 ? LCP : 1];
+    int ln_cpt = 0;
+    if constexpr (LNF == 2) {
+        static_assert(NT % BM == 0 && TPR >= 2 && TPR <= 16, "row statistics: 2-16 threads per row");
+        ln_cpt = ep.stats_chunks / TPR;
+        const float2 *src = ep.stats_in + (size_t)min(m0 + tid / TPR, M - 1) * ep.stats_chunks +
+                            (tid % TPR) * ln_cpt;
+#pragma unroll
+        for (int c = 0; c < LCP; c++) ln_ch[c] = src[min(c, ln_cpt - 1)];
+    }
+    auto ln_acc = [&](auto par) {
+        if constexpr (LN_LOOP) {
+            const f32x4 *ra = ra_sets[decltype(par)::value];
+#pragma unroll
+            for (int i = 0; i < ACH; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float d = ra[i][e] - ln_sh[i];
+                    ln_s1[i] += d;
+                    ln_s2[i] = fmaf(d, d, ln_s2[i]);
+                }
         }
     };
 
@@ -392,8 +471,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     };
 
     const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
-    gload(kbeg);
-    lstore(0);
+    gload(kbeg, P0{});
+    lstore(0, P0{});
     __syncthreads();
     if constexpr (EXACT) {
         // Branch-free slice loop: the last iteration reloads its own slice
@@ -404,10 +483,17 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
         // next slice go out first.  Unrolled by two, so that the buffer of
         // each slice is a constant and every LDS address is a loop-invariant
         // register plus an immediate.
-        auto slice = [&](int t, int cur) {
-            gload(kbeg + min(t + 1, ktiles - 1) * BK);
+        // LNF: slice t's own elements (register set t % 2, loaded during
+        // slice t - 1 and already waited for by its LDS stores) go into the
+        // LayerNorm sums while this slice's loads fill the other set; the
+        // sums are free to sit anywhere in the slice.
+        auto slice = [&](int t, auto curc) {
+            constexpr int cur = decltype(curc)::value;
+            using Next = std::integral_constant<int, cur ^ 1>;
+            gload(kbeg + min(t + 1, ktiles - 1) * BK, Next{});
+            ln_acc(curc);
             compute(cur);
-            lstore(cur ^ 1);
+            lstore(cur ^ 1, Next{});
             constexpr int NR = FM + FN, NM = 4 * FM * FN, NL = ACH + BCH;
             __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);  // k-step 0 fragments
             __builtin_amdgcn_sched_group_barrier(0x020, NL, 0);  // next slice, global
@@ -432,17 +518,17 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
         };
         int t = 0;
         for (; t + 1 < ktiles; t += 2) {
-            slice(t, 0);
-            slice(t + 1, 1);
+            slice(t, P0{});
+            slice(t + 1, P1{});
         }
-        if (t < ktiles) slice(t, 0);
+        if (t < ktiles) slice(t, P0{});
     } else {
         for (int t = 0; t < ktiles; t++) {
             const int cur = t & 1;
             const bool next = t + 1 < ktiles;
-            if (next) gload(kbeg + (t + 1) * BK);
+            if (next) gload(kbeg + (t + 1) * BK, P0{});
             compute(cur);
-            if (next) lstore(cur ^ 1);
+            if (next) lstore(cur ^ 1, P0{});
             __syncthreads();
         }
     }
@@ -481,6 +567,18 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                     for (int r = 0; r < 4; r++)
                         __hip_atomic_store(mine + ((i * FN + j) * 4 + r) * NT + tid, acc[i][j][r],
                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            constexpr int LS = 2 * LA;  // LayerNorm sums per thread and piece
+            const size_t stats_base = (size_t)tail_u * ep.tail_splits * LS * NT;
+            if constexpr (LN_LOOP) {
+                float *st = ep.tail_stats + stats_base + (size_t)piece * LS * NT;
+#pragma unroll
+                for (int i = 0; i < LA; i++) {
+                    __hip_atomic_store(st + (2 * i) * NT + tid, ln_s1[i], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(st + (2 * i + 1) * NT + tid, ln_s2[i], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             if (tid == 0)
@@ -495,6 +593,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
             constexpr int MAXS = 4;  // tail_splits <= 4 (tail_plan)
             const float *parts = ep.partial + tile_base;
             float pv[MAXS][PER];
+            float ps[MAXS][LN_LOOP ? LS : 1];
 #pragma unroll
             for (int p = 0; p < MAXS; p++) {
                 if (p < ep.tail_splits) {
@@ -502,9 +601,33 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                     for (int e = 0; e < PER; e++)
                         pv[p][e] = __hip_atomic_load(parts + (size_t)(p * PER + e) * NT + tid, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
+                    if constexpr (LN_LOOP) {
+#pragma unroll
+                        for (int e = 0; e < LS; e++)
+                            ps[p][e] = __hip_atomic_load(ep.tail_stats + stats_base + (size_t)(p * LS + e) * NT + tid,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
                 } else {
 #pragma unroll
                     for (int e = 0; e < PER; e++) pv[p][e] = 0.0f;
+                    if constexpr (LN_LOOP) {
+#pragma unroll
+                        for (int e = 0; e < LS; e++) ps[p][e] = 0.0f;
+                    }
+                }
+            }
+            if constexpr (LN_LOOP) {
+#pragma unroll
+                for (int i = 0; i < LA; i++) {
+                    float s1 = ps[0][2 * i], s2 = ps[0][2 * i + 1];
+#pragma unroll
+                    for (int p = 1; p < MAXS; p++)
+                        if (p < ep.tail_splits) {
+                            s1 += ps[p][2 * i];
+                            s2 += ps[p][2 * i + 1];
+                        }
+                    ln_s1[i] = s1;
+                    ln_s2[i] = s2;
                 }
             }
 #pragma unroll
@@ -523,6 +646,52 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
             if (tid == 0) __hip_atomic_store(ep.tail_cnt + tail_u, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+
+    // LayerNorm fold: each row's sums are spread over CPR consecutive lanes;
+    // after the reduction one lane per row writes (mean, rstd) to LDS for the
+    // epilogue.  LDS is free: every slice ends with a barrier, after the
+    // last fragment reads.  mean = s + S1/K, var = S2/K - (S1/K)^2 about the
+    // shift s.
+    if constexpr (LN_LOOP) {
+#pragma unroll
+        for (int i = 0; i < ACH; i++) {
+            ln_s1[i] = group_sum<CPR>(ln_s1[i]);
+            ln_s2[i] = group_sum<CPR>(ln_s2[i]);
+        }
+        float2 *lns = reinterpret_cast<float2 *>(smem);
+        if (tid % CPR == 0) {
+            const float kf = (float)K;
+#pragma unroll
+            for (int i = 0; i < ACH; i++) {
+                const float m1 = ln_s1[i] / kf;
+                const float var = fmaxf(ln_s2[i] / kf - m1 * m1, 0.0f);
+                lns[(tid + i * NT) / CPR] = float2{ln_sh[i] + m1, 1.0f / sqrtf(var + ep.ln_eps)};
+            }
+        }
+        __syncthreads();
+    } else if constexpr (LNF == 2) {
+        // Chan's merge of equal-width chunks: mean = mean of the chunk
+        // means, M2 = sum of (M2_c + w * (mean_c - mean)^2).
+        const float w = (float)(K / ep.stats_chunks);
+        float msum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < LCP; c++)
+            if (c < ln_cpt) msum += ln_ch[c].x;
+        const float mean = group_sum<TPR>(msum) / (float)ep.stats_chunks;
+        float q = 0.0f;
+#pragma unroll
+        for (int c = 0; c < LCP; c++)
+            if (c < ln_cpt) {
+                const float d = ln_ch[c].x - mean;
+                q += fmaf(w * d, d, ln_ch[c].y);
+            }
+        q = group_sum<TPR>(q);
+        if (tid % TPR == 0)
+            reinterpret_cast<float2 *>(smem)[tid / TPR] = float2{mean, 1.0f / sqrtf(q / (float)K + ep.ln_eps)};
+        __syncthreads();
+    }
+    // (mean, rstd) of tile row r (LNF only).
+    auto ln_row = [&](int r) { return reinterpret_cast<const float2 *>(smem)[r]; };
 
     // C fragment layout: register r of lane l holds row 4*(l/16)+r, column l%16.
     const int rbase = m0 + wm * TM + 4 * lh;
@@ -622,9 +791,12 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
         const int d0 = colw % 64;       // 0 or 32 (32-wide tile) / 0 (64-wide)
         float *dst = group == 0 ? ep.q : (group == 1 ? ep.k : ep.v);
         const bool rope = ep.rot != nullptr && group < 2;
-        float bias[FN];
+        float bias[FN], lc[FN];
 #pragma unroll
-        for (int j = 0; j < FN; j++) bias[j] = ep.bias[colw + j * 16 + li];
+        for (int j = 0; j < FN; j++) {
+            bias[j] = ep.bias[colw + j * 16 + li];
+            if constexpr (LN_ANY) lc[j] = ep.ln_c[colw + j * 16 + li];
+        }
         // Rotation (sin, cos) of every row this lane stores, read before any
         // store from clamped rows so that the reads overlap.
         float2 rot[FM][4][FN / 2];
@@ -651,8 +823,14 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                 if (row >= M) continue;
                 const int img = row / ep.tokens, t = row % ep.tokens;
                 float vals[FN];
+                if constexpr (LN_ANY) {
+                    const float2 st = ln_row(row - m0);
 #pragma unroll
-                for (int j = 0; j < FN; j++) vals[j] = add_rn(acc[i][j][r], bias[j]);
+                    for (int j = 0; j < FN; j++) vals[j] = fmaf(st.y, fmaf(-st.x, lc[j], acc[i][j][r]), bias[j]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < FN; j++) vals[j] = add_rn(acc[i][j][r], bias[j]);
+                }
                 if (rope) {
                     // rope::rotate_half (src/rope.rs:84-93): dims (i, i+16) of
                     // each 32-wide axis half sit in fragments (2h, 2h+1).
@@ -674,14 +852,23 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
         // store, so the reads overlap instead of each waiting behind the
         // bounds branch of its element.
         const int cbase = n0 + wn * TN + li;
-        float bias[FN], gamma[FN];
+        float bias[FN], gamma[FN], lc[FN];
 #pragma unroll
         for (int j = 0; j < FN; j++) {
             const int col = min(cbase + j * 16, N - 1);
             bias[j] = load_or(ep.bias, (const float *)ep.c, col, 0.0f);
             gamma[j] = load_or(ep.gamma, (const float *)ep.c, col, 1.0f);
+            if constexpr (LN_ANY) lc[j] = ep.ln_c[col];
+        }
+        float2 lnst[LN_ANY ? FM : 1][4];
+        if constexpr (LN_ANY) {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) lnst[i][r] = ln_row(wm * TM + 4 * lh + i * 16 + r);
         }
         float resid[EPI == Epi::Residual ? FM : 1][FN][4];
+        float outv[EPI == Epi::Residual ? FM : 1][FN][4];
         if constexpr (EPI == Epi::Residual) {
 #pragma unroll
             for (int i = 0; i < FM; i++)
@@ -712,7 +899,10 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                         if (!WHOLE && row >= M) continue;
                         const size_t idx = (size_t)row * N + col;
                         float v = acc[i][j][r];
-                        if (ep.bias) v = add_rn(v, bias[j]);
+                        if constexpr (LN_ANY)
+                            v = fmaf(lnst[i][r].y, fmaf(-lnst[i][r].x, lc[j], v), bias[j]);
+                        else if (ep.bias)
+                            v = add_rn(v, bias[j]);
                         if constexpr (EPI == Epi::Store) {
                             if (ep.gamma) v = mul_rn(v, gamma[j]);
                             ep.c[idx] = v;
@@ -723,7 +913,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                                 ep.c[idx] = idx < ep.tail_start ? gelu_avx512_form(v) : gelu_scalar_form(v);
                         } else {
                             if (ep.gamma) v = mul_rn(v, gamma[j]);
-                            ep.c[idx] = add_rn(resid[i][j][r], v);
+                            const float o = add_rn(resid[i][j][r], v);
+                            ep.c[idx] = o;
+                            if constexpr (EPI == Epi::Residual) outv[i][j][r] = o;
                         }
                     }
             }
@@ -734,6 +926,26 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
             store_all(std::true_type{});
         else
             store_all(std::false_type{});
+        // Row statistics of the updated rows for the next sub-layer's
+        // LayerNorm fold: a wave's 32 columns are one chunk; the 16 lanes of
+        // a lane group hold a row's 32 values (two per lane), so the chunk's
+        // mean and M2 take two 16-lane sums (two passes, no cancellation).
+        if constexpr (EPI == Epi::Residual && TN == 32) {
+            if (ep.stats_out && n0 + wn * TN < N) {
+                const int chunk = (n0 + wn * TN) / 32;
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float mean = group_sum<16>(outv[i][0][r] + outv[i][1][r]) * (1.0f / 32.0f);
+                        const float d0 = outv[i][0][r] - mean, d1 = outv[i][1][r] - mean;
+                        const float m2 = group_sum<16>(fmaf(d0, d0, d1 * d1));
+                        const int row = rbase + i * 16 + r;
+                        if (li == 0 && row < M)
+                            ep.stats_out[(size_t)row * ep.stats_chunks + chunk] = float2{mean, m2};
+                    }
+            }
+        }
     }
 }
 
@@ -891,10 +1103,11 @@ int use_xcd_order(const GemmArgs &g) {
     return g.m > 1024 || g.k >= 2048;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, int CONV = 0>
+template <int BM, int BN, int BK, int WM, int WN, Epi EPI, bool SPLIT, bool EXACT, int CONV = 0,
+          int LNF = 0>
 hipError_t launch_tile(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, int splits, int kps) {
     constexpr size_t lds = gemm_lds_bytes<BM, BN, BK>();
-    auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, SPLIT, EXACT, CONV>;
+    auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, SPLIT, EXACT, CONV, false, LNF>;
     static std::atomic<uint64_t> configured{0};
     if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
     dim3 grid((unsigned)((g.n + BN - 1) / BN), (unsigned)((g.m + BM - 1) / BM), (unsigned)splits);
@@ -1041,14 +1254,15 @@ bool tail_plan(const GemmArgs &g, const Tile &t, TailPlan *plan, int only_splits
     return true;
 }
 
-template <Epi EPI>
+template <Epi EPI, int LNF = 0>
 hipError_t launch_tail(hipStream_t s, const GemmArgs &g, EpiArgs ep, const TailPlan &p) {
     constexpr int BM = 64, BN = 64, BK = 32, WM = 2, WN = 2;
     constexpr size_t lds = gemm_lds_bytes<BM, BN, BK>();
-    auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, false, true, 0, true>;
+    auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, false, true, 0, true, LNF>;
     static std::atomic<uint64_t> configured{0};
     if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
     ep.partial = g.tail_ws;
+    ep.tail_stats = g.tail_stats;
     ep.tail_cnt = g.tail_cnt;
     ep.tail_full = p.full;
     ep.tail_splits = p.splits;
@@ -1060,8 +1274,50 @@ hipError_t launch_tail(hipStream_t s, const GemmArgs &g, EpiArgs ep, const TailP
     return hipGetLastError();
 }
 
+// LayerNorm-folded Gelu / Qkv GEMM (ln_fold_c set): whole slices and no K
+// split, on the 64x128x64 tile where the per-shape table picks it and the
+// 64x64x32 tile otherwise (with the balanced tail for Gelu when tail_plan
+// takes it).  The row statistics come from the producer's chunk statistics
+// (stats_in) when given in a shape the tile takes, else from the A slices.
+template <Epi EPI, int LNF>
+hipError_t launch_lnf(hipStream_t s, const GemmArgs &g, const EpiArgs &ep, bool wide) {
+    if constexpr (EPI == Epi::Gelu) {
+        TailPlan p;
+        if (!wide && g.tail_stats && tail_plan(g, Tile{64, 64, 32, 2, 2}, &p))
+            return launch_tail<EPI, LNF>(s, g, ep, p);
+    }
+    if (wide) return launch_tile<64, 128, 64, 2, 4, EPI, false, true, 0, LNF>(s, g, ep, 1, (int)g.k);
+    return launch_tile<64, 64, 32, 2, 2, EPI, false, true, 0, LNF>(s, g, ep, 1, (int)g.k);
+}
+
+template <Epi EPI>
+hipError_t dispatch_lnf(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
+    Tile t;
+    int splits;
+    if (!tile_override(&t, &splits)) default_tile(g, &t, &splits);
+    const bool wide = t.bm == 64 && t.bn == 128 && t.bk == 64 && t.wm == 2 && t.wn == 4;
+    const int bk = wide ? 64 : 32;
+    if (g.k == 0 || g.k % bk != 0 || !g.bias) return hipErrorInvalidValue;
+    const size_t tpr = wide ? 8 : 4;  // threads per tile row (NT / BM)
+    const size_t ch = g.stats_chunks;
+    // VESTRA_HIP_LN_STATS=0 ignores the producer's statistics (A/B studies
+    // and tests of both forms; read per call).
+    const char *env = std::getenv("VESTRA_HIP_LN_STATS");
+    const bool use_in = !(env && env[0] == '0');
+    if (use_in && g.stats_in && ch && g.k == ch * 32 && ch % tpr == 0 && ch / tpr <= 8) {
+        ep.stats_in = reinterpret_cast<const float2 *>(g.stats_in);
+        ep.stats_chunks = (int)ch;
+        return launch_lnf<EPI, 2>(s, g, ep, wide);
+    }
+    return launch_lnf<EPI, 1>(s, g, ep, wide);
+}
+
 template <Epi EPI>
 hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
+    if (g.ln_fold_c) {
+        if constexpr (EPI == Epi::Gelu || EPI == Epi::Qkv) return dispatch_lnf<EPI>(s, g, ep);
+        return hipErrorInvalidValue;
+    }
     Tile t;
     int splits;
     const bool overridden = tile_override(&t, &splits);
@@ -1069,11 +1325,23 @@ hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     if (EPI == Epi::Qkv) splits = 1;
     const int table_splits = !overridden && splits > 1 ? splits : 0;
     if (splits > 1 && (g.ws == nullptr || g.ws_floats < (size_t)splits * g.m * g.n)) splits = 1;
+    // Residual with stats_out: the 64-wide tiles of the tail and of the
+    // unsplit 64 x 64 x 32 launch (32-column wave tiles) also write the row
+    // statistics of the updated rows (reported through stats_written).
+    auto with_stats = [&](EpiArgs e) {
+        if (EPI == Epi::Residual && g.stats_out && g.n % 32 == 0 && g.n / 32 == g.stats_chunks) {
+            e.stats_out = reinterpret_cast<float2 *>(g.stats_out);
+            e.stats_chunks = (int)g.stats_chunks;
+            if (g.stats_written) *g.stats_written = true;
+        }
+        return e;
+    };
+    if (g.stats_written) *g.stats_written = false;
     if constexpr (EPI != Epi::Qkv) {
         // Store, GELU and Residual: the last piece of a tail tile runs the
         // epilogue once (a Residual tile adds its residual exactly once).
         TailPlan p;
-        if (splits == 1 && tail_plan(g, t, &p)) return launch_tail<EPI>(s, g, ep, p);
+        if (splits == 1 && tail_plan(g, t, &p)) return launch_tail<EPI>(s, g, with_stats(ep), p);
         // A long-K launch that the table splits, whose 64 x 64 grid has
         // fewer tiles than CUs (fc2 at 865 tokens: 168 tiles): every tile as
         // K pieces, the last piece of each summing them in order and running
@@ -1084,11 +1352,13 @@ hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
         // fused fc2 reduction and LayerNorm still splits K that way).
         if (table_splits && g.k % ((size_t)table_splits * t.bk) == 0 &&
             tail_plan(g, Tile{64, 64, 32, 2, 2}, &p, table_splits) && p.full == 0)
-            return launch_tail<EPI>(s, g, ep, p);
+            return launch_tail<EPI>(s, g, with_stats(ep), p);
     }
     if (splits == 1) {
-        hipError_t e = run_cfg<EPI, false>(s, g, ep, t, 1);
+        const bool narrow_wave = t.bm == 64 && t.bn == 64 && t.bk == 32 && t.wm == 2 && t.wn == 2;
+        hipError_t e = run_cfg<EPI, false>(s, g, narrow_wave ? with_stats(ep) : ep, t, 1);
         if (e == hipErrorInvalidValue) {
+            if (g.stats_written) *g.stats_written = false;
             default_tile(g, &t, &splits);
             e = run_cfg<EPI, false>(s, g, ep, t, 1);
         }
@@ -1209,6 +1479,8 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs &g) {
     ep.tokens = (int)g.tokens;
     ep.heads = (int)g.heads;
     ep.rot = g.rot;
+    ep.ln_c = g.ln_fold_c;
+    ep.ln_eps = g.ln_fold_eps;
     size_t total = g.m * g.n;
     ep.tail_start = total - total % 16;
     if (g.conv_in_c && g.conv_ih) {

@@ -131,6 +131,25 @@ struct GemmArgs {
     size_t tail_ws_floats = 0;
     unsigned *tail_cnt = nullptr;
     size_t tail_cnt_n = 0;
+    // Per-row LayerNorm sums of LayerNorm-folded tail pieces (kTailStatFloats).
+    float *tail_stats = nullptr;
+    // Gelu / Qkv only: a is the raw input of a pre-norm sub-layer and the
+    // GEMM computes LayerNorm(a) . W^T + b as rstd * (a . bt^T - mean * c) +
+    // bias, with bt = W diag(ln gamma), ln_fold_c = c[n] = sum_k bt[n][k] and
+    // bias = b + W . ln beta prepared by the caller; the row statistics are
+    // taken inside the GEMM (epsilon ln_fold_eps).  K % 64 == 0.
+    const float *ln_fold_c = nullptr;
+    float ln_fold_eps = 0.0f;
+    // Row statistics per 32-column chunk, (mean, M2) float pairs
+    // [m][stats_chunks]: a Residual GEMM with stats_out writes them for the
+    // rows it updates when its tile allows (n == 32 * stats_chunks; then
+    // *stats_written = true), and a LayerNorm-folded GEMM with stats_in takes
+    // its row statistics from them (k == 32 * stats_chunks) instead of from
+    // its A slices.
+    float *stats_out = nullptr;
+    const float *stats_in = nullptr;
+    size_t stats_chunks = 0;
+    bool *stats_written = nullptr;
     // Residual only: also write LayerNorm(c) row by row to ln_out (the next
     // sub-layer's input), fused into the split-K reduction when possible.
     const float *ln_gamma = nullptr, *ln_beta = nullptr;
@@ -164,6 +183,7 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs &g);
 // Sizes of the balanced-tail workspace (GemmArgs::tail_ws / tail_cnt).
 constexpr size_t kTailTiles = 512;
 constexpr size_t kTailFloats = kTailTiles * 4 * 64 * 64;
+constexpr size_t kTailStatFloats = kTailTiles * 4 * 4 * 256;
 
 // ---- Q8_0 (k_q8.hip) --------------------------------------------------------
 // x [rows][k] -> block-major Q8_0: qs [k/32][rows][32] int8, d [k/32][rows] f16 bits

@@ -147,6 +147,10 @@ struct Lin {
     float *wt = nullptr;  // [N][K]
     float *bias = nullptr;
     float *gamma = nullptr;  // null = unit LayerScale
+    // Set for a projection that takes a LayerNorm of its input folded in
+    // (prepare_lin_ln): wt = W diag(ln gamma), bias = b + W . ln beta and
+    // ln_c[n] = sum_k wt[n][k].
+    float *ln_c = nullptr;
 };
 
 // A projection with Q8_0 weights: W^T [N][K] as block-major blocks,
@@ -213,7 +217,7 @@ struct vh_block {
         if (!rt) return;
         hipSetDevice(rt->device);
         for (Lin *l : {&qkv, &proj, &fc1, &fc2})
-            for (float *p : {l->wt, l->bias, l->gamma})
+            for (float *p : {l->wt, l->bias, l->gamma, l->ln_c})
                 if (p) hipFreeAsync(p, rt->stream);
         for (Q8Lin *l : {&qqkv, &qproj, &qfc1, &qfc2}) l->release(rt->stream);
         for (float *p : {ln1_g, ln1_b, ln2_g, ln2_b, qn_g, qn_b, kn_g, kn_b})
@@ -379,7 +383,7 @@ vh_status splitk_workspace(RtState &s, size_t m, size_t n, float **out, size_t *
 vh_status tail_workspace(RtState &s, vh::GemmArgs &g) {
     if (!s.tw) {
         hipStreamSynchronize(s.stream);
-        hipError_t e = hipMalloc(&s.tw, vh::kTailFloats * sizeof(float));
+        hipError_t e = hipMalloc(&s.tw, (vh::kTailFloats + vh::kTailStatFloats) * sizeof(float));
         if (e == hipSuccess) e = hipMalloc(&s.tcnt, vh::kTailTiles * sizeof(unsigned));
         if (e == hipSuccess) e = hipMemsetAsync(s.tcnt, 0, vh::kTailTiles * sizeof(unsigned), s.stream);
         if (e != hipSuccess) {
@@ -392,6 +396,7 @@ vh_status tail_workspace(RtState &s, vh::GemmArgs &g) {
     }
     g.tail_ws = s.tw;
     g.tail_ws_floats = vh::kTailFloats;
+    g.tail_stats = s.tw + vh::kTailFloats;
     g.tail_cnt = s.tcnt;
     g.tail_cnt_n = vh::kTailTiles;
     return VH_OK;
@@ -447,6 +452,41 @@ vh_status prepare_lin(RtState &s, size_t K, size_t N, const float *w, const floa
     return VH_OK;
 }
 
+// A projection of LayerNorm(x) (gamma g, beta be) prepared for the folded
+// form LayerNorm(x) . W^T + b = rstd * (x . W'^T - mean * c) + b' (see
+// GemmArgs::ln_fold_c): W'[n][k] = W[k][n] * g[k] (w is [K][N], in x out),
+// c[n] = sum_k W'[n][k] and b'[n] = b[n] + sum_k W[k][n] * be[k], both sums in
+// double over the rounded W' and the given W.
+vh_status prepare_lin_ln(RtState &s, size_t K, size_t N, const float *w, const float *bias,
+                         const float *ln_g, const float *ln_b, Lin *L) {
+    if (!w || !bias || !ln_g || !ln_b) return null_arg("prepare_lin_ln");
+    std::vector<float> wt(K * N), c(N), bp(N);
+    for (size_t n = 0; n < N; n++) {
+        double cs = 0.0, bs = (double)bias[n];
+        for (size_t k = 0; k < K; k++) {
+            const float wv = w[k * N + n];
+            const float f = wv * ln_g[k];
+            wt[n * K + k] = f;
+            cs += (double)f;
+            bs += (double)wv * (double)ln_b[k];
+        }
+        c[n] = (float)cs;
+        bp[n] = (float)bs;
+    }
+    vh_status st = upload_array(s, wt.data(), K * N, &L->wt, "linear weight upload");
+    if (!st) st = upload_array(s, bp.data(), N, &L->bias, "linear bias upload");
+    if (!st) st = upload_array(s, c.data(), N, &L->ln_c, "linear LayerNorm fold upload");
+    if (st) {
+        for (float *p : {L->wt, L->bias, L->ln_c})
+            if (p) hipFreeAsync(p, s.stream);
+        *L = Lin{};
+        return st;
+    }
+    L->K = K;
+    L->N = N;
+    return VH_OK;
+}
+
 // LayerNorm applied to the rows a Residual GEMM has just updated.
 struct RowNorm {
     const float *gamma, *beta;
@@ -454,8 +494,17 @@ struct RowNorm {
     float eps;
 };
 
+// Row statistics passed between a Residual GEMM and the LayerNorm-folded
+// GEMM after it: (mean, M2) per 32-column chunk of each row (GemmArgs).
+struct ChunkStats {
+    const float *in = nullptr;  // the input rows' statistics, or null
+    float *out = nullptr;       // where a Residual GEMM writes them, or null
+    bool *written = nullptr;    // set when out was written
+};
+
 vh_status run_lin(RtState &s, const Lin &L, const float *in, size_t rows, vh::Epi epi, float *c,
-                  const char *name, const RowNorm *norm = nullptr) {
+                  const char *name, const RowNorm *norm = nullptr, float fold_eps = 0.0f,
+                  const ChunkStats &cs = ChunkStats{}) {
     vh::GemmArgs g{};
     g.a = in;
     g.bt = L.wt;
@@ -472,14 +521,32 @@ vh_status run_lin(RtState &s, const Lin &L, const float *in, size_t rows, vh::Ep
         g.ln_out = norm->out;
         g.ln_eps = norm->eps;
     }
+    g.ln_fold_c = L.ln_c;
+    g.ln_fold_eps = fold_eps;
+    if (cs.in && L.K % 32 == 0) {
+        g.stats_in = cs.in;
+        g.stats_chunks = L.K / 32;
+    }
+    if (cs.out && L.N % 32 == 0) {
+        g.stats_out = cs.out;
+        g.stats_chunks = L.N / 32;
+        g.stats_written = cs.written;
+    }
     TRY(splitk_workspace(s, rows, L.N, &g.ws, &g.ws_floats));
     TRY(tail_workspace(s, g));
     return launch(s, name, [&] { return vh::launch_gemm(s.stream, g); });
 }
 
 vh_status run_qkv(RtState &s, const Lin &L, const float *in, size_t images, size_t tokens,
-                  size_t heads, const float *rot, float *q, float *k, float *v) {
+                  size_t heads, const float *rot, float *q, float *k, float *v, float fold_eps = 0.0f,
+                  const float *stats_in = nullptr) {
     vh::GemmArgs g{};
+    g.ln_fold_c = L.ln_c;
+    g.ln_fold_eps = fold_eps;
+    if (stats_in && L.K % 32 == 0) {
+        g.stats_in = stats_in;
+        g.stats_chunks = L.K / 32;
+    }
     g.a = in;
     g.bt = L.wt;
     g.m = images * tokens;
@@ -1860,20 +1927,19 @@ vh_status upload_small(RtState &s, const float *h, size_t n, float **out, const 
     return upload_array(s, h, n, out, what);
 }
 
-// One pre-norm block, in place on x.  With h_ready the caller has already
-// written LayerNorm1(x) into the block workspace (the previous block's fc2
-// fused it); with next, this block's fc2 writes the next block's
-// LayerNorm1(x) there the same way (f32 blocks only: a Q8_0 block ignores
-// next).
+// One pre-norm block, in place on x.  x_stats (encoder runs): on entry,
+// whether the block workspace holds x's row statistics (the previous f32
+// block's fc2 wrote them); on return, whether this block's fc2 did.
 vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size_t tokens,
-                    const int64_t *pos, float freq, float eps, bool h_ready = false,
-                    const vh_block *next = nullptr) {
+                    const int64_t *pos, float freq, float eps, bool *x_stats = nullptr) {
     const size_t M = images * tokens;
     const size_t D = kDim;
     float *ws = nullptr;
-    TRY(workspace(s, M * (5 * D + kMlp), &ws));
-    float *h = ws, *q = h + M * D, *k = q + M * D, *v = k + M * D, *att = v + M * D,
-          *f = att + M * D;
+    TRY(workspace(s, M * (4 * D + kMlp + 2 * (D / 32)), &ws));
+    float *q = ws, *k = q + M * D, *v = k + M * D, *att = v + M * D, *f = att + M * D;
+    float *rs = f + M * kMlp;  // row statistics [M][D / 32][mean, M2]
+    const bool stats_in = x_stats && *x_stats;
+    if (x_stats) *x_stats = false;
     const float *rot = nullptr;
     if (pos) {
         TRY(rope_table(s, pos, tokens, 64, freq, &rot));
@@ -1885,12 +1951,10 @@ vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size
     }
     if (b.q8) {
         // Q8_0 projections: each GEMM takes Q8_0 rows, so the LayerNorms
-        // write Q8_0 directly (h_ready: the previous f32 block left
-        // LayerNorm1(x) in h, which is quantised), and fc2 leaves the next
-        // block's LayerNorm1 to that block.
+        // write Q8_0 directly.
         const RowNorm ln1{b.ln1_g, b.ln1_b, nullptr, eps};
-        const float *qin = h_ready ? h : x;
-        const RowNorm *n1 = h_ready ? nullptr : &ln1;
+        const float *qin = x;
+        const RowNorm *n1 = &ln1;
         if (b.qn_g) {
             TRY(run_q8_qkv(s, b.qqkv, qin, images, tokens, nullptr, q, k, v, n1));
             TRY(launch(s, "qk_norm_rope", [&] {
@@ -1934,30 +1998,32 @@ vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size
                                         vh::Epi::Residual, b.qfc2.bias, b.qfc2.gamma);
         });
     }
-    if (!h_ready)
-        TRY(launch(s, "layernorm", [&] {
-            return vh::launch_layernorm(s.stream, x, b.ln1_g, b.ln1_b, h, M, D, eps);
-        }));
+    // f32 projections: LayerNorm 1 and 2 are folded into the QKV and fc1
+    // GEMMs (prepare_lin_ln), which read the residual stream x itself and
+    // take its row statistics from the Residual GEMM before them when that
+    // one wrote them (the out-projection for fc1, the previous block's fc2
+    // for QKV), else from their own A slices.
+    const float *qkv_stats = stats_in ? rs : nullptr;
     if (b.qn_g) {
         // Late block: QKV with bias only, then LayerNorm of every 64-wide Q
         // and K head row fused with the RoPE (src/specialized.rs:278-316).
-        TRY(run_qkv(s, b.qkv, h, images, tokens, kHeads, nullptr, q, k, v));
+        TRY(run_qkv(s, b.qkv, x, images, tokens, kHeads, nullptr, q, k, v, eps, qkv_stats));
         TRY(launch(s, "qk_norm_rope", [&] {
             return vh::launch_qk_norm_rope(s.stream, q, k, b.qn_g, b.qn_b, b.kn_g, b.kn_b, rot,
                                            M * kHeads, tokens, eps);
         }));
     } else {
-        TRY(run_qkv(s, b.qkv, h, images, tokens, kHeads, rot, q, k, v));
+        TRY(run_qkv(s, b.qkv, x, images, tokens, kHeads, rot, q, k, v, eps, qkv_stats));
     }
     TRY(flash(s, q, k, v, att, images * kHeads, tokens, kHeads, true));
-    const RowNorm ln2{b.ln2_g, b.ln2_b, h, eps};
-    TRY(run_lin(s, b.proj, att, M, vh::Epi::Residual, x, "gemm_proj_residual_ln", &ln2));
-    TRY(run_lin(s, b.fc1, h, M, vh::Epi::Gelu, f, "gemm_fc1_gelu"));
-    if (next) {
-        const RowNorm ln1{next->ln1_g, next->ln1_b, h, eps};
-        return run_lin(s, b.fc2, f, M, vh::Epi::Residual, x, "gemm_fc2_residual_ln", &ln1);
-    }
-    return run_lin(s, b.fc2, f, M, vh::Epi::Residual, x, "gemm_fc2_residual");
+    bool proj_stats = false;
+    TRY(run_lin(s, b.proj, att, M, vh::Epi::Residual, x, "gemm_proj_residual", nullptr, 0.0f,
+                ChunkStats{nullptr, rs, &proj_stats}));
+    TRY(run_lin(s, b.fc1, x, M, vh::Epi::Gelu, f, "gemm_fc1_gelu", nullptr, eps,
+                ChunkStats{proj_stats ? rs : nullptr, nullptr, nullptr}));
+    if (!x_stats) return run_lin(s, b.fc2, f, M, vh::Epi::Residual, x, "gemm_fc2_residual");
+    return run_lin(s, b.fc2, f, M, vh::Epi::Residual, x, "gemm_fc2_residual", nullptr, 0.0f,
+                   ChunkStats{nullptr, rs, x_stats});
 }
 
 vh_status check_block_x(const vh_tensor *x, size_t images, size_t tokens) {
@@ -1997,9 +2063,9 @@ static vh_status block_prepare(const vh_runtime *rt, const vh_block_params *p, b
         if (!st) st = prepare_q8_from_f32(s, kDim, kMlp, p->w_fc1, p->b_fc1, nullptr, &b->qfc1);
         if (!st) st = prepare_q8_from_f32(s, kMlp, kDim, p->w_fc2, p->b_fc2, p->ls2, &b->qfc2);
     } else {
-        st = prepare_lin(s, kDim, 3 * kDim, p->w_qkv, p->b_qkv, nullptr, &b->qkv);
+        st = prepare_lin_ln(s, kDim, 3 * kDim, p->w_qkv, p->b_qkv, p->ln1_gamma, p->ln1_beta, &b->qkv);
         if (!st) st = prepare_lin(s, kDim, kDim, p->w_proj, p->b_proj, p->ls1, &b->proj);
-        if (!st) st = prepare_lin(s, kDim, kMlp, p->w_fc1, p->b_fc1, nullptr, &b->fc1);
+        if (!st) st = prepare_lin_ln(s, kDim, kMlp, p->w_fc1, p->b_fc1, p->ln2_gamma, p->ln2_beta, &b->fc1);
         if (!st) st = prepare_lin(s, kMlp, kDim, p->w_fc2, p->b_fc2, p->ls2, &b->fc2);
     }
     if (!st) st = upload_small(s, p->ln1_gamma, kDim, &b->ln1_g, "ln1 gamma");
@@ -2063,11 +2129,14 @@ extern "C" vh_status vh_encoder_run(const vh_runtime *rt, const vh_block *const 
     RtState &s = *rt->s;
     TRY(set_device(s));
     if (images * tokens == 0) return VH_OK;
-    // An f32 block's fc2 writes the next block's LayerNorm1; a Q8_0 block's
-    // does not, so the block after it normalises its own input.
-    for (size_t i = 0; i < layers; i++)
+    // Each f32 block's fc2 leaves the row statistics of its output for the
+    // next block's QKV (a Q8_0 block normalises its own input).
+    bool x_stats = false;
+    for (size_t i = 0; i < layers; i++) {
+        if (blocks[i]->q8) x_stats = false;
         TRY(block_run(s, *blocks[i], x->ptr, images, tokens, pos_yx, rope_frequency, epsilon,
-                      i > 0 && !blocks[i - 1]->q8, i + 1 < layers ? blocks[i + 1] : nullptr));
+                      blocks[i]->q8 ? nullptr : &x_stats));
+    }
     return VH_OK;
     GUARD_END
 }

@@ -57,14 +57,16 @@ def positions_global(rows: int, cols: int, special: int = 1) -> np.ndarray:
 
 def block_weights(seed: int, layer: int = 0, layerscale: float | str = LAYERSCALE,
                   w_std: float = 0.02, b_std: float = 0.02,
-                  qk_norm: bool = False) -> dict[str, np.ndarray]:
+                  qk_norm: bool = False, ln_affine: bool = False) -> dict[str, np.ndarray]:
     """Seeded block parameters: weights N(0, w_std^2) row-major [in, out],
     biases N(0, b_std^2), LayerNorm gamma=1 / beta=0, LayerScale constant,
     or, with layerscale="uniform", drawn per channel from U(0.1, 1) (large
     enough that every branch moves the residual stream well past f32
     rounding, so an encoder's output checks each layer's arithmetic).
     With qk_norm (DA3's late blocks) the 64-wide Q and K LayerNorms get
-    gamma ~ 1 + N(0, 0.1^2) and beta ~ N(0, b_std^2)."""
+    gamma ~ 1 + N(0, 0.1^2) and beta ~ N(0, b_std^2).  With ln_affine the
+    block's two LayerNorms get gamma ~ U(0.5, 1.5) and beta ~ N(0, 0.1^2)
+    per channel instead of 1 and 0."""
     def n(tid, count, std):
         return seeded.normal(seeded.tensor_seed(seed, layer, tid), count, std)
 
@@ -82,16 +84,24 @@ def block_weights(seed: int, layer: int = 0, layerscale: float | str = LAYERSCAL
             "k_norm_gamma": (1.0 + n(11, HEAD_DIM, 0.1)).astype(np.float32),
             "k_norm_beta": n(12, HEAD_DIM, b_std),
         }
+    def ln(tid_g, tid_b):
+        if not ln_affine:
+            return np.ones(DIM, np.float32), np.zeros(DIM, np.float32)
+        u = seeded.uniform01(seeded.tensor_seed(seed, layer, tid_g), DIM)
+        return (0.5 + u).astype(np.float32), n(tid_b, DIM, 0.1)
+
+    ln1_g, ln1_b = ln(13, 14)
+    ln2_g, ln2_b = ln(15, 16)
     return extra | {
-        "ln1_gamma": np.ones(DIM, np.float32),
-        "ln1_beta": np.zeros(DIM, np.float32),
+        "ln1_gamma": ln1_g,
+        "ln1_beta": ln1_b,
         "w_qkv": n(1, DIM * QKV, w_std),
         "b_qkv": n(2, QKV, b_std),
         "w_proj": n(3, DIM * DIM, w_std),
         "b_proj": n(4, DIM, b_std),
         "ls1": ls(20),
-        "ln2_gamma": np.ones(DIM, np.float32),
-        "ln2_beta": np.zeros(DIM, np.float32),
+        "ln2_gamma": ln2_g,
+        "ln2_beta": ln2_b,
         "w_fc1": n(5, DIM * MLP, w_std),
         "b_fc1": n(6, MLP, b_std),
         "w_fc2": n(7, MLP * DIM, w_std),
