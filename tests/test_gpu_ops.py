@@ -269,6 +269,52 @@ def test_residual_epilogue_vs_oracle(rt, m, k):
     assert max_rel(rt.download_f32(xt), exp) <= 1e-5
 
 
+@pytest.mark.parametrize("m,k,mode", [(865, 768, "default"), (97, 768, "default"),
+                                      (1000, 256, "default"), (3460, 768, "forced"),
+                                      (865, 3072, "forced"), (200, 384, "forced")])
+def test_kgroup_residual_gemm(rt, monkeypatch, m, k, mode):
+    """The Residual GEMM with K split over four wave groups of one workgroup
+    and summed through LDS (64 x 48 tiles; the out-projection's default at
+    M <= 1024, K <= 1024, forced with VESTRA_HIP_GEMM_KGROUP=1 elsewhere).
+    Bars: within 1e-5 of the oracle, the GEMM part inside the fp32 error
+    bound of a float64 product, identical run to run, and different in some
+    bits from unsplit 64 x 64 tiles (so the kernel ran; the balanced tail's
+    four K pieces can sum in the same order), with LayerScale and ragged
+    row tiles (97, 865, 1000 rows)."""
+    n = 768
+    a = seeded.normal(71 + m, m * k)
+    w = seeded.normal(72, k * n, 0.02)
+    bias = seeded.normal(73, n, 0.02)
+    ls = (0.1 + 0.9 * seeded.uniform01(75, n)).astype(np.float32)
+    x = seeded.normal(74 + m, m * n)
+    lin = rt.prepare_linear_f32(k, n, w, bias, ls)
+    at = rt.upload_f32(a)
+    monkeypatch.setenv("VESTRA_HIP_GEMM_KGROUP", "1" if mode == "forced" else "")
+    xt = rt.upload_f32(x)
+    lin.run_residual(at, m, xt)
+    got = rt.download_f32(xt)
+    again = rt.upload_f32(x)
+    lin.run_residual(at, m, again)
+    assert_bits_equal(rt.download_f32(again), got, "kgroup rerun")
+    y = O.linear_bias_scale(a, w, bias, ls, m, n, k)
+    assert max_rel(got, O.kernels_add(x, y)) <= 1e-5
+    ref = a.reshape(m, k).astype(np.float64) @ w.reshape(k, n).astype(np.float64)
+    bound = k * 6e-8 * (np.abs(a.reshape(m, k)).astype(np.float64) @ np.abs(w.reshape(k, n)))
+    acc = ((got.reshape(m, n).astype(np.float64) - x.reshape(m, n)) / ls - bias)
+    # acc carries the rounding of the bias add, the LayerScale and the
+    # residual add too: a few ulps of |x| and |y| on top of the GEMM bound.
+    slack = 4e-7 * (np.abs(x.reshape(m, n)) / ls + np.abs(ref) + np.abs(bias))
+    assert np.all(np.abs(acc - ref) <= bound + slack)
+    monkeypatch.setenv("VESTRA_HIP_GEMM_KGROUP", "0")
+    monkeypatch.setenv("VESTRA_HIP_GEMM_TAIL", "0")
+    monkeypatch.setenv("VESTRA_HIP_GEMM_TILE", "64x64x32x2x2x1")
+    other = rt.upload_f32(x)
+    lin.run_residual(at, m, other)
+    other = rt.download_f32(other)
+    assert max_rel(got - x, other - x) <= 1e-5
+    assert (got.view(np.uint32) != other.view(np.uint32)).any()
+
+
 @pytest.mark.parametrize("images, rows, cols, rope", [
     (1, 24, 36, False), (1, 24, 36, True), (4, 24, 36, True), (1, 48, 72, True)],
     ids=["865", "865-rope", "4x865-rope", "3457-rope"])

@@ -949,6 +949,233 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     }
 }
 
+// Residual GEMM with the K split inside the workgroup, for the narrow short-K
+// projection (the out-projection: 865 x 768 x 768, whose 64 x 64 tiles are
+// fewer than the CUs).  KG groups of WM x WN waves share a BM x BN tile;
+// group g runs K range [g K / KG, (g + 1) K / KG) through its own double-
+// buffered LDS stages (the slice layout and fragment schedule of
+// gemm_nt_kernel), all groups in step at one barrier per slice.  The groups'
+// partial tiles are then summed through LDS in group order (a fixed order,
+// so the result does not depend on timing) and group 0 applies the Residual
+// epilogue: c = c + (acc + bias) * gamma.  With 64 x 48 tiles the 865-row
+// projection is 224 workgroups of 8 waves, one per CU, two waves per SIMD,
+// with no partial tiles leaving the CU and no second launch.  With
+// ep.stats_out (WN == 1), group 0 also writes each row's (mean, M2) over the
+// tile's BN columns: one chunk per tile.
+template <int BM, int BN, int BK, int WM, int WN, int KG>
+__global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kgroup_kernel(const float *__restrict__ A,
+                                                                      const float *__restrict__ Bt,
+                                                                      int M, int N, int K, EpiArgs ep) {
+    constexpr int GT = WM * WN * 64;  // threads per K group
+    constexpr int CPR = BK / 4;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int FM = TM / 16, FN = TN / 16;
+    constexpr int ACH = BM * CPR / GT, BCH = BN * CPR / GT;
+    static_assert((BM * CPR) % GT == 0 && (BN * CPR) % GT == 0 && ACH >= 1 && BCH >= 1, "tile / thread mismatch");
+    static_assert(TM % 16 == 0 && TN % 16 == 0 && BK % 16 == 0, "fragment shape");
+    constexpr int STAGE = (BM + BN) * BK;
+    static_assert((KG - 1) * FM * FN * 4 * GT <= KG * 2 * STAGE, "partials fit the staging LDS");
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kg = wave / (WM * WN), gw = wave % (WM * WN), gt = tid % GT;
+    const int li = lane & 15, lh = lane >> 4;
+    const int wm = gw / WN, wn = gw % WN;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kper = K / KG, kbeg = kg * kper, ktiles = kper / BK;
+    float *gsm = smem + kg * 2 * STAGE;  // this group's two stages
+
+    f32x4 ra[1][ACH], rb[1][BCH];
+    auto gload = [&](int k0, int set) {
+#pragma unroll
+        for (int i = 0; i < ACH; i++) {
+            const int c = gt + i * GT, row = c / CPR, kq = (c % CPR) * 4;
+            ra[set][i] = *reinterpret_cast<const f32x4 *>(A + (size_t)min(m0 + row, M - 1) * K + k0 + kq);
+        }
+#pragma unroll
+        for (int i = 0; i < BCH; i++) {
+            const int c = gt + i * GT, row = c / CPR, kq = (c % CPR) * 4;
+            rb[set][i] = *reinterpret_cast<const f32x4 *>(Bt + (size_t)min(n0 + row, N - 1) * K + k0 + kq);
+        }
+    };
+    auto lstore = [&](int buf, int set) {
+        float *as = gsm + buf * STAGE;
+        float *bs = as + BM * BK;
+#pragma unroll
+        for (int i = 0; i < ACH; i++) {
+            const int c = gt + i * GT;
+            *reinterpret_cast<f32x4 *>(&as[swz<BK>(c / CPR, c % CPR)]) = ra[set][i];
+        }
+#pragma unroll
+        for (int i = 0; i < BCH; i++) {
+            const int c = gt + i * GT;
+            *reinterpret_cast<f32x4 *>(&bs[swz<BK>(c / CPR, c % CPR)]) = rb[set][i];
+        }
+    };
+    const int rbase = m0 + wm * TM + 4 * lh;
+    const int cbase = n0 + wn * TN + li;
+    float bias[FN], gamma[FN], resid[FM][FN][4];
+    // The epilogue's reads (group 0): bias, LayerScale and the residual tile.
+    auto epi_loads = [&]() {
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int col = min(cbase + j * 16, N - 1);
+            bias[j] = load_or(ep.bias, (const float *)ep.c, col, 0.0f);
+            gamma[j] = load_or(ep.gamma, (const float *)ep.c, col, 1.0f);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    resid[i][j][r] =
+                        ep.c[(size_t)min(rbase + i * 16 + r, M - 1) * N + min(cbase + j * 16, N - 1)];
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    int goff[BK / 16];
+#pragma unroll
+    for (int q = 0; q < BK / 16; q++) goff[q] = 4 * ((4 * q + lh) ^ (li & (CPR - 1)));
+    f32x4 a[2][FM], b[2][FN];
+    auto fetch = [&](int slot, int buf, int kk) {
+        const float *as = gsm + buf * STAGE + (wm * TM + li) * BK + goff[kk / 16];
+        const float *bs = gsm + buf * STAGE + BM * BK + (wn * TN + li) * BK + goff[kk / 16];
+#pragma unroll
+        for (int i = 0; i < FM; i++) a[slot][i] = *reinterpret_cast<const f32x4 *>(as + i * 16 * BK);
+#pragma unroll
+        for (int j = 0; j < FN; j++) b[slot][j] = *reinterpret_cast<const f32x4 *>(bs + j * 16 * BK);
+    };
+    auto compute = [&](int buf) {
+        fetch(0, buf, 0);
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 16) {
+            const int cur = (kk / 16) & 1;
+            if (kk + 16 < BK) fetch(cur ^ 1, buf, kk + 16);
+#pragma unroll
+            for (int st = 0; st < 4; st++)
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++) acc[i][j] = mfma16x16x4(a[cur][i][st], b[cur][j][st], acc[i][j]);
+        }
+    };
+
+    gload(kbeg, 0);
+    lstore(0, 0);
+    __syncthreads();
+    // The slice loop of gemm_nt_kernel's whole-slice path: the last slice
+    // reloads its own slice into the idle buffer, so every iteration is one
+    // basic block whose order is pinned (next slice's global loads first,
+    // fragment reads and LDS stores in the shadow of the MFMAs).
+    auto slice = [&](int t, int cur) {
+        gload(kbeg + min(t + 1, ktiles - 1) * BK, 0);
+        compute(cur);
+        lstore(cur ^ 1, 0);
+        constexpr int NR = FM + FN, NM = 4 * FM * FN, NL = ACH + BCH;
+        __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, NL, 0);
+#pragma unroll
+        for (int st = 0; st + 1 < BK / 16; st++) {
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
+        }
+        constexpr int NW = NL < NM ? NL : NM;
+#pragma unroll
+        for (int r = 0; r < NW; r++) {
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, NM - NW, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, NL - NW, 0);
+        __syncthreads();
+    };
+    int t = 0;
+    for (; t + 1 < ktiles; t += 2) {
+        slice(t, 0);
+        slice(t + 1, 1);
+    }
+    if (t < ktiles) slice(t, 0);
+
+    // Group g > 0 leaves its partial tile in LDS (thread-major: conflict-
+    // free), and group 0 adds them in group order.  The staging LDS is free:
+    // every slice ends with a barrier after its last fragment reads.
+    constexpr int PER = FM * FN * 4;
+    if (kg > 0) {
+        float *mine = smem + (size_t)(kg - 1) * PER * GT;
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) mine[((i * FN + j) * 4 + r) * GT + gt] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int g = 1; g < KG; g++) {
+        const float *part = smem + (size_t)(g - 1) * PER * GT;
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[i][j][r] = acc[i][j][r] + part[((i * FN + j) * 4 + r) * GT + gt];
+    }
+
+    // Residual epilogue (gemm_nt_kernel's), reads issued before any store.
+    epi_loads();
+    float outv[FM][FN][4];
+    wait_vmem_all();
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float v = acc[i][j][r];
+                if (ep.bias) v = add_rn(v, bias[j]);
+                if (ep.gamma) v = mul_rn(v, gamma[j]);
+                const float o = add_rn(resid[i][j][r], v);
+                outv[i][j][r] = o;
+                const int row = rbase + i * 16 + r, col = cbase + j * 16;
+                if (row < M && col < N) ep.c[(size_t)row * N + col] = o;
+            }
+    if constexpr (WN == 1) {
+        // The 16 lanes of a lane group hold a row's BN values (FN per lane):
+        // mean and M2 over the tile's columns by two 16-lane sums.
+        if (ep.stats_out) {
+            const int chunk = n0 / BN;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < FN; j++) sum += outv[i][j][r];
+                    const float mean = group_sum<16>(sum) / (float)BN;
+                    float m2 = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < FN; j++) {
+                        const float d = outv[i][j][r] - mean;
+                        m2 = fmaf(d, d, m2);
+                    }
+                    m2 = group_sum<16>(m2);
+                    const int row = rbase + i * 16 + r;
+                    if (li == 0 && row < M) ep.stats_out[(size_t)row * ep.stats_chunks + chunk] = float2{mean, m2};
+                }
+        }
+    }
+}
+
 // Sums the split-K partials in split order, then applies the epilogue; four
 // consecutive outputs per thread (N % 4 == 0) so every access is a 16-byte
 // vector.
@@ -1274,6 +1501,36 @@ hipError_t launch_tail(hipStream_t s, const GemmArgs &g, EpiArgs ep, const TailP
     return hipGetLastError();
 }
 
+// The in-workgroup split-K Residual GEMM (gemm_kgroup_kernel, 64 x 48 tiles,
+// 4 K groups of 2 waves): taken for M <= 1024, K <= 1024 (the out-projection
+// at 865 tokens: 15.6 us as the balanced tail's 504 pieces), when N % 48 == 0
+// and each group has at least two whole 32-wide slices.
+// VESTRA_HIP_GEMM_KGROUP=0 never takes it, =1 whenever the shape allows.
+bool use_kgroup(const GemmArgs &g) {
+    constexpr size_t KG = 4, BK = 32;
+    if (g.n % 48 != 0 || g.k % (KG * BK) != 0 || g.k / KG < 2 * BK || g.m > INT32_MAX) return false;
+    const char *env = std::getenv("VESTRA_HIP_GEMM_KGROUP");  // per call (tests switch it)
+    if (env && env[0] == '0') return false;
+    if (env && env[0] == '1') return true;
+    return g.m <= 1024 && g.k <= 1024;
+}
+
+hipError_t launch_kgroup(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
+    constexpr int BM = 64, BN = 48, BK = 32, WM = 2, WN = 1, KG = 4;
+    constexpr size_t lds = (size_t)KG * 2 * (BM + BN) * BK * sizeof(float);
+    auto kernel = gemm_kgroup_kernel<BM, BN, BK, WM, WN, KG>;
+    static std::atomic<uint64_t> configured{0};
+    if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
+    if (g.stats_out) {
+        ep.stats_out = reinterpret_cast<float2 *>(g.stats_out);
+        ep.stats_chunks = (int)(g.n / BN);
+        if (g.stats_out_chunks) *g.stats_out_chunks = ep.stats_chunks;
+    }
+    dim3 grid((unsigned)(g.n / BN), (unsigned)((g.m + BM - 1) / BM));
+    kernel<<<grid, WM * WN * KG * 64, lds, s>>>(g.a, g.bt, (int)g.m, (int)g.n, (int)g.k, ep);
+    return hipGetLastError();
+}
+
 // LayerNorm-folded Gelu / Qkv GEMM (ln_fold_c set): whole slices and no K
 // split, on the 64x128x64 tile where the per-shape table picks it and the
 // 64x64x32 tile otherwise (with the balanced tail for Gelu when tail_plan
@@ -1299,12 +1556,12 @@ hipError_t dispatch_lnf(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     const int bk = wide ? 64 : 32;
     if (g.k == 0 || g.k % bk != 0 || !g.bias) return hipErrorInvalidValue;
     const size_t tpr = wide ? 8 : 4;  // threads per tile row (NT / BM)
-    const size_t ch = g.stats_chunks;
+    const size_t ch = g.stats_in_chunks;
     // VESTRA_HIP_LN_STATS=0 ignores the producer's statistics (A/B studies
     // and tests of both forms; read per call).
     const char *env = std::getenv("VESTRA_HIP_LN_STATS");
     const bool use_in = !(env && env[0] == '0');
-    if (use_in && g.stats_in && ch && g.k == ch * 32 && ch % tpr == 0 && ch / tpr <= 8) {
+    if (use_in && g.stats_in && ch && g.k % ch == 0 && ch % tpr == 0 && ch / tpr <= 8) {
         ep.stats_in = reinterpret_cast<const float2 *>(g.stats_in);
         ep.stats_chunks = (int)ch;
         return launch_lnf<EPI, 2>(s, g, ep, wide);
@@ -1327,16 +1584,19 @@ hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     if (splits > 1 && (g.ws == nullptr || g.ws_floats < (size_t)splits * g.m * g.n)) splits = 1;
     // Residual with stats_out: the 64-wide tiles of the tail and of the
     // unsplit 64 x 64 x 32 launch (32-column wave tiles) also write the row
-    // statistics of the updated rows (reported through stats_written).
+    // statistics of the updated rows (chunks per row in stats_out_chunks).
     auto with_stats = [&](EpiArgs e) {
-        if (EPI == Epi::Residual && g.stats_out && g.n % 32 == 0 && g.n / 32 == g.stats_chunks) {
+        if (EPI == Epi::Residual && g.stats_out && g.n % 32 == 0) {
             e.stats_out = reinterpret_cast<float2 *>(g.stats_out);
-            e.stats_chunks = (int)g.stats_chunks;
-            if (g.stats_written) *g.stats_written = true;
+            e.stats_chunks = (int)(g.n / 32);
+            if (g.stats_out_chunks) *g.stats_out_chunks = e.stats_chunks;
         }
         return e;
     };
-    if (g.stats_written) *g.stats_written = false;
+    if (g.stats_out_chunks) *g.stats_out_chunks = 0;
+    if constexpr (EPI == Epi::Residual) {
+        if (!overridden && use_kgroup(g)) return launch_kgroup(s, g, ep);
+    }
     if constexpr (EPI != Epi::Qkv) {
         // Store, GELU and Residual: the last piece of a tail tile runs the
         // epilogue once (a Residual tile adds its residual exactly once).
@@ -1358,7 +1618,7 @@ hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
         const bool narrow_wave = t.bm == 64 && t.bn == 64 && t.bk == 32 && t.wm == 2 && t.wn == 2;
         hipError_t e = run_cfg<EPI, false>(s, g, narrow_wave ? with_stats(ep) : ep, t, 1);
         if (e == hipErrorInvalidValue) {
-            if (g.stats_written) *g.stats_written = false;
+            if (g.stats_out_chunks) *g.stats_out_chunks = 0;
             default_tile(g, &t, &splits);
             e = run_cfg<EPI, false>(s, g, ep, t, 1);
         }

@@ -140,16 +140,17 @@ struct GemmArgs {
     // taken inside the GEMM (epsilon ln_fold_eps).  K % 64 == 0.
     const float *ln_fold_c = nullptr;
     float ln_fold_eps = 0.0f;
-    // Row statistics per 32-column chunk, (mean, M2) float pairs
-    // [m][stats_chunks]: a Residual GEMM with stats_out writes them for the
-    // rows it updates when its tile allows (n == 32 * stats_chunks; then
-    // *stats_written = true), and a LayerNorm-folded GEMM with stats_in takes
-    // its row statistics from them (k == 32 * stats_chunks) instead of from
-    // its A slices.
+    // Row statistics per chunk of equal-width column ranges, (mean, M2)
+    // float pairs [m][chunks]: a Residual GEMM with stats_out (room for
+    // m * n / 16 pairs) writes them for the rows it updates when its tile
+    // allows, and reports the chunks per row in *stats_out_chunks (0: none
+    // written); a LayerNorm-folded GEMM with stats_in (stats_in_chunks per
+    // row, k a multiple of it) takes its row statistics from them instead of
+    // from its A slices.
     float *stats_out = nullptr;
+    int *stats_out_chunks = nullptr;
     const float *stats_in = nullptr;
-    size_t stats_chunks = 0;
-    bool *stats_written = nullptr;
+    size_t stats_in_chunks = 0;
     // Residual only: also write LayerNorm(c) row by row to ln_out (the next
     // sub-layer's input), fused into the split-K reduction when possible.
     const float *ln_gamma = nullptr, *ln_beta = nullptr;

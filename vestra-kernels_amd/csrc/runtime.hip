@@ -495,11 +495,12 @@ struct RowNorm {
 };
 
 // Row statistics passed between a Residual GEMM and the LayerNorm-folded
-// GEMM after it: (mean, M2) per 32-column chunk of each row (GemmArgs).
+// GEMM after it: (mean, M2) per column chunk of each row (GemmArgs).
 struct ChunkStats {
-    const float *in = nullptr;  // the input rows' statistics, or null
-    float *out = nullptr;       // where a Residual GEMM writes them, or null
-    bool *written = nullptr;    // set when out was written
+    const float *in = nullptr;     // the input rows' statistics, or null
+    size_t in_chunks = 0;          // chunks per row of in
+    float *out = nullptr;          // where a Residual GEMM writes them, or null
+    int *out_chunks = nullptr;     // chunks per row written to out (0: none)
 };
 
 vh_status run_lin(RtState &s, const Lin &L, const float *in, size_t rows, vh::Epi epi, float *c,
@@ -523,14 +524,13 @@ vh_status run_lin(RtState &s, const Lin &L, const float *in, size_t rows, vh::Ep
     }
     g.ln_fold_c = L.ln_c;
     g.ln_fold_eps = fold_eps;
-    if (cs.in && L.K % 32 == 0) {
+    if (cs.in && cs.in_chunks) {
         g.stats_in = cs.in;
-        g.stats_chunks = L.K / 32;
+        g.stats_in_chunks = cs.in_chunks;
     }
-    if (cs.out && L.N % 32 == 0) {
+    if (cs.out) {
         g.stats_out = cs.out;
-        g.stats_chunks = L.N / 32;
-        g.stats_written = cs.written;
+        g.stats_out_chunks = cs.out_chunks;
     }
     TRY(splitk_workspace(s, rows, L.N, &g.ws, &g.ws_floats));
     TRY(tail_workspace(s, g));
@@ -539,13 +539,13 @@ vh_status run_lin(RtState &s, const Lin &L, const float *in, size_t rows, vh::Ep
 
 vh_status run_qkv(RtState &s, const Lin &L, const float *in, size_t images, size_t tokens,
                   size_t heads, const float *rot, float *q, float *k, float *v, float fold_eps = 0.0f,
-                  const float *stats_in = nullptr) {
+                  const float *stats_in = nullptr, size_t stats_in_chunks = 0) {
     vh::GemmArgs g{};
     g.ln_fold_c = L.ln_c;
     g.ln_fold_eps = fold_eps;
-    if (stats_in && L.K % 32 == 0) {
+    if (stats_in && stats_in_chunks) {
         g.stats_in = stats_in;
-        g.stats_chunks = L.K / 32;
+        g.stats_in_chunks = stats_in_chunks;
     }
     g.a = in;
     g.bt = L.wt;
@@ -1927,19 +1927,20 @@ vh_status upload_small(RtState &s, const float *h, size_t n, float **out, const 
     return upload_array(s, h, n, out, what);
 }
 
-// One pre-norm block, in place on x.  x_stats (encoder runs): on entry,
-// whether the block workspace holds x's row statistics (the previous f32
-// block's fc2 wrote them); on return, whether this block's fc2 did.
+// One pre-norm block, in place on x.  x_chunks (encoder runs): on entry,
+// the chunks per row of x's row statistics in the block workspace (the
+// previous f32 block's fc2 wrote them; 0: none); on return, those this
+// block's fc2 wrote.
 vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size_t tokens,
-                    const int64_t *pos, float freq, float eps, bool *x_stats = nullptr) {
+                    const int64_t *pos, float freq, float eps, int *x_chunks = nullptr) {
     const size_t M = images * tokens;
     const size_t D = kDim;
     float *ws = nullptr;
-    TRY(workspace(s, M * (4 * D + kMlp + 2 * (D / 32)), &ws));
+    TRY(workspace(s, M * (4 * D + kMlp + 2 * (D / 16)), &ws));
     float *q = ws, *k = q + M * D, *v = k + M * D, *att = v + M * D, *f = att + M * D;
-    float *rs = f + M * kMlp;  // row statistics [M][D / 32][mean, M2]
-    const bool stats_in = x_stats && *x_stats;
-    if (x_stats) *x_stats = false;
+    float *rs = f + M * kMlp;  // row statistics [M][chunks <= D / 16][mean, M2]
+    const int in_chunks = x_chunks ? *x_chunks : 0;
+    if (x_chunks) *x_chunks = 0;
     const float *rot = nullptr;
     if (pos) {
         TRY(rope_table(s, pos, tokens, 64, freq, &rot));
@@ -2003,27 +2004,27 @@ vh_status block_run(RtState &s, const vh_block &b, float *x, size_t images, size
     // take its row statistics from the Residual GEMM before them when that
     // one wrote them (the out-projection for fc1, the previous block's fc2
     // for QKV), else from their own A slices.
-    const float *qkv_stats = stats_in ? rs : nullptr;
+    const float *qkv_stats = in_chunks ? rs : nullptr;
     if (b.qn_g) {
         // Late block: QKV with bias only, then LayerNorm of every 64-wide Q
         // and K head row fused with the RoPE (src/specialized.rs:278-316).
-        TRY(run_qkv(s, b.qkv, x, images, tokens, kHeads, nullptr, q, k, v, eps, qkv_stats));
+        TRY(run_qkv(s, b.qkv, x, images, tokens, kHeads, nullptr, q, k, v, eps, qkv_stats, in_chunks));
         TRY(launch(s, "qk_norm_rope", [&] {
             return vh::launch_qk_norm_rope(s.stream, q, k, b.qn_g, b.qn_b, b.kn_g, b.kn_b, rot,
                                            M * kHeads, tokens, eps);
         }));
     } else {
-        TRY(run_qkv(s, b.qkv, x, images, tokens, kHeads, rot, q, k, v, eps, qkv_stats));
+        TRY(run_qkv(s, b.qkv, x, images, tokens, kHeads, rot, q, k, v, eps, qkv_stats, in_chunks));
     }
     TRY(flash(s, q, k, v, att, images * kHeads, tokens, kHeads, true));
-    bool proj_stats = false;
+    int proj_chunks = 0;
     TRY(run_lin(s, b.proj, att, M, vh::Epi::Residual, x, "gemm_proj_residual", nullptr, 0.0f,
-                ChunkStats{nullptr, rs, &proj_stats}));
+                ChunkStats{nullptr, 0, rs, &proj_chunks}));
     TRY(run_lin(s, b.fc1, x, M, vh::Epi::Gelu, f, "gemm_fc1_gelu", nullptr, eps,
-                ChunkStats{proj_stats ? rs : nullptr, nullptr, nullptr}));
-    if (!x_stats) return run_lin(s, b.fc2, f, M, vh::Epi::Residual, x, "gemm_fc2_residual");
+                ChunkStats{proj_chunks ? rs : nullptr, (size_t)proj_chunks, nullptr, nullptr}));
+    if (!x_chunks) return run_lin(s, b.fc2, f, M, vh::Epi::Residual, x, "gemm_fc2_residual");
     return run_lin(s, b.fc2, f, M, vh::Epi::Residual, x, "gemm_fc2_residual", nullptr, 0.0f,
-                   ChunkStats{nullptr, rs, x_stats});
+                   ChunkStats{nullptr, 0, rs, x_chunks});
 }
 
 vh_status check_block_x(const vh_tensor *x, size_t images, size_t tokens) {
@@ -2131,11 +2132,11 @@ extern "C" vh_status vh_encoder_run(const vh_runtime *rt, const vh_block *const 
     if (images * tokens == 0) return VH_OK;
     // Each f32 block's fc2 leaves the row statistics of its output for the
     // next block's QKV (a Q8_0 block normalises its own input).
-    bool x_stats = false;
+    int x_chunks = 0;
     for (size_t i = 0; i < layers; i++) {
-        if (blocks[i]->q8) x_stats = false;
+        if (blocks[i]->q8) x_chunks = 0;
         TRY(block_run(s, *blocks[i], x->ptr, images, tokens, pos_yx, rope_frequency, epsilon,
-                      blocks[i]->q8 ? nullptr : &x_stats));
+                      blocks[i]->q8 ? nullptr : &x_chunks));
     }
     return VH_OK;
     GUARD_END
