@@ -195,6 +195,27 @@ def test_fc1_gelu_epilogue_vs_oracle(rt, m):
     assert max_rel(got, exp) <= 1e-5
 
 
+def test_fused_gelu_epilogue_form(rt):
+    """The f32 GEMM's GELU epilogue evaluates the A&S 7.1.26 erf of
+    Kernels::gelu with the hardware reciprocal and exp2.  Through an identity
+    weight (every product but one is an exact zero, so the GEMM returns its
+    input) it is compared with the oracle's exact GELU over [-12, 12], the
+    edges of the erf polynomial and signed zeros: within 1e-6 * max(1, |v|)
+    absolutely, against 0.47 for a GELU that dropped the 1/sqrt(2) (a
+    plausible slip; computed with the oracle)."""
+    k = n = 256
+    v = np.concatenate([np.linspace(-12.0, 12.0, 256 * 250), [0.0, -0.0, 1e-30, -1e-30, 4.0, -4.0]])
+    v = np.concatenate([v, np.zeros((-v.size) % k)]).astype(np.float32)
+    m = v.size // k
+    lin = rt.prepare_linear_f32(k, n, np.eye(k, dtype=np.float32).reshape(-1), np.zeros(n, np.float32))
+    got = rt.download_f32(lin.run_gelu(rt.upload_f32(v), m))
+    exp = O.kernels_gelu(v)
+    err = np.abs(got.astype(np.float64) - exp) / np.maximum(1.0, np.abs(v))
+    assert err.max() <= 1e-6
+    slip = np.abs(O.kernels_gelu((v * np.float32(np.sqrt(2.0))).astype(np.float32)) - exp)
+    assert (slip / np.maximum(1.0, np.abs(v))).max() >= 0.1
+
+
 @pytest.mark.parametrize("m,k,n", [(865, 768, 3072), (400, 768, 3072), (865, 768, 3136),
                                    (300, 256, 4096), (3460, 768, 3072), (865, 480, 3072)])
 def test_gemm_balanced_tail(rt, monkeypatch, m, k, n):

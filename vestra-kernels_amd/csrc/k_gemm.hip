@@ -23,7 +23,8 @@
 //
 // Epilogues (all separately rounded, as the reference's):
 //   Store    : c = (acc + bias) * gamma          (CudaLinearF32::run)
-//   Gelu     : c = gelu(acc + bias)              (fc1, Kernels::gelu forms)
+//   Gelu     : c = gelu(acc + bias)              (fc1; the A&S 7.1.26 erf of
+//              Kernels::gelu on the hardware reciprocal and exp2, gelu_fast_form)
 //   Residual : c = c + (acc + bias) * gamma      (out-proj / fc2 + residual)
 //   Qkv      : head-major Q/K/V with bias and the 2-D RoPE rotation of Q, K
 //
@@ -56,7 +57,6 @@ struct EpiArgs {
     float *q, *k, *v;
     int tokens, heads;
     const float *rot;
-    size_t tail_start;
     float *partial;  // split-K: raw partial tiles [split][M][N]
     // Implicit convolution (CONV kernels): Bt is a zero-padded channel-last
     // image [rows][conv_in_c] and row n of the GEMM's Bt for k-slice k0 is
@@ -102,7 +102,7 @@ __device__ __forceinline__ void epilogue_store(const EpiArgs &ep, size_t idx, in
         if (ep.gamma) v = mul_rn(v, ep.gamma[col]);
         ep.c[idx] = v;
     } else if constexpr (EPI == Epi::Gelu) {
-        ep.c[idx] = idx < ep.tail_start ? gelu_avx512_form(v) : gelu_scalar_form(v);
+        ep.c[idx] = gelu_fast_form(v);
     } else {
         if (ep.gamma) v = mul_rn(v, ep.gamma[col]);
         ep.c[idx] = add_rn(ep.c[idx], v);
@@ -881,10 +881,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                     }
         }
         wait_vmem_all();  // then the guarded stores need no waits between them
-        // A tile wholly inside C and, for GELU, wholly before the scalar
-        // tail (the last n % 16 values, tail_start on) stores without
-        // per-element checks; the decision is per tile, so the branch is
-        // uniform and the arithmetic is the same either way.
+        // A tile wholly inside C stores without per-element checks; the
+        // decision is per tile, so the branch is uniform and the arithmetic
+        // is the same either way.
         auto store_all = [&](auto whole_tile) {
             constexpr bool WHOLE = decltype(whole_tile)::value;
 #pragma unroll
@@ -907,10 +906,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                             if (ep.gamma) v = mul_rn(v, gamma[j]);
                             ep.c[idx] = v;
                         } else if constexpr (EPI == Epi::Gelu) {
-                            if constexpr (WHOLE)
-                                ep.c[idx] = gelu_avx512_form(v);
-                            else
-                                ep.c[idx] = idx < ep.tail_start ? gelu_avx512_form(v) : gelu_scalar_form(v);
+                            ep.c[idx] = gelu_fast_form(v);
                         } else {
                             if (ep.gamma) v = mul_rn(v, gamma[j]);
                             const float o = add_rn(resid[i][j][r], v);
@@ -920,8 +916,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                     }
             }
         };
-        const bool whole = m0 + BM <= M && n0 + BN <= N &&
-                           (EPI != Epi::Gelu || (size_t)(m0 + BM - 1) * N + (n0 + BN - 1) < ep.tail_start);
+        const bool whole = m0 + BM <= M && n0 + BN <= N;
         if (whole)
             store_all(std::true_type{});
         else
@@ -1234,7 +1229,7 @@ __global__ __launch_bounds__(256) void splitk_reduce4_kernel(int M, int N, EpiAr
         float t = v[e];
         if (ep.bias) t = add_rn(t, b[e]);
         if constexpr (EPI == Epi::Gelu) {
-            o[e] = i4 * 4 + e < ep.tail_start ? gelu_avx512_form(t) : gelu_scalar_form(t);
+            o[e] = gelu_fast_form(t);
         } else {
             if (ep.gamma) t = mul_rn(t, g[e]);
             o[e] = EPI == Epi::Residual ? add_rn(x[e], t) : t;
@@ -1741,8 +1736,6 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs &g) {
     ep.rot = g.rot;
     ep.ln_c = g.ln_fold_c;
     ep.ln_eps = g.ln_fold_eps;
-    size_t total = g.m * g.n;
-    ep.tail_start = total - total % 16;
     if (g.conv_in_c && g.conv_ih) {
         if (g.epi != Epi::Store || g.conv_kw == 0 || g.conv_ow == 0 || g.conv_iw == 0 ||
             g.conv_stride == 0 || g.n % g.conv_ow != 0 || g.k % (g.conv_in_c * g.conv_kw) != 0)
