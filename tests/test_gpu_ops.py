@@ -294,14 +294,13 @@ def test_residual_epilogue_vs_oracle(rt, m, k):
                                       (1000, 256, "default"), (3460, 768, "forced"),
                                       (865, 3072, "forced"), (200, 384, "forced")])
 def test_kgroup_residual_gemm(rt, monkeypatch, m, k, mode):
-    """The Residual GEMM with K split over four wave groups of one workgroup
-    and summed through LDS (64 x 48 tiles; the out-projection's default at
+    """The Residual GEMM with K split over two wave groups of one workgroup
+    and summed through LDS (32 x 96 tiles; the out-projection's default at
     M <= 1024, K <= 1024, forced with VESTRA_HIP_GEMM_KGROUP=1 elsewhere).
     Bars: within 1e-5 of the oracle, the GEMM part inside the fp32 error
     bound of a float64 product, identical run to run, and different in some
-    bits from unsplit 64 x 64 tiles (so the kernel ran; the balanced tail's
-    four K pieces can sum in the same order), with LayerScale and ragged
-    row tiles (97, 865, 1000 rows)."""
+    bits from unsplit 64 x 64 tiles (so the kernel ran), with LayerScale and
+    ragged row tiles (97, 865, 1000 rows)."""
     n = 768
     a = seeded.normal(71 + m, m * k)
     w = seeded.normal(72, k * n, 0.02)

@@ -952,11 +952,11 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
 // gemm_nt_kernel), all groups in step at one barrier per slice.  The groups'
 // partial tiles are then summed through LDS in group order (a fixed order,
 // so the result does not depend on timing) and group 0 applies the Residual
-// epilogue: c = c + (acc + bias) * gamma.  With 64 x 48 tiles the 865-row
-// projection is 224 workgroups of 8 waves, one per CU, two waves per SIMD,
-// with no partial tiles leaving the CU and no second launch.  With
-// ep.stats_out (WN == 1), group 0 also writes each row's (mean, M2) over the
-// tile's BN columns: one chunk per tile.
+// epilogue: c = c + (acc + bias) * gamma.  With 32 x 96 tiles, 2 x 2 waves
+// and two K groups the 865-row projection is 224 workgroups of 8 waves, one
+// per CU, two waves per SIMD, with no partial tiles leaving the CU and no
+// second launch.  With ep.stats_out, group 0 also writes each row's (mean,
+// M2) over each wave's TN columns: one chunk per wave column.
 template <int BM, int BN, int BK, int WM, int WN, int KG>
 __global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kgroup_kernel(const float *__restrict__ A,
                                                                       const float *__restrict__ Bt,
@@ -1144,11 +1144,11 @@ __global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kgroup_kernel(const floa
                 const int row = rbase + i * 16 + r, col = cbase + j * 16;
                 if (row < M && col < N) ep.c[(size_t)row * N + col] = o;
             }
-    if constexpr (WN == 1) {
-        // The 16 lanes of a lane group hold a row's BN values (FN per lane):
-        // mean and M2 over the tile's columns by two 16-lane sums.
+    {
+        // The 16 lanes of a lane group hold a row's TN values of this wave
+        // (FN per lane): mean and M2 over them by two 16-lane sums.
         if (ep.stats_out) {
-            const int chunk = n0 / BN;
+            const int chunk = (n0 + wn * TN) / TN;
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -1156,7 +1156,7 @@ __global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kgroup_kernel(const floa
                     float sum = 0.0f;
 #pragma unroll
                     for (int j = 0; j < FN; j++) sum += outv[i][j][r];
-                    const float mean = group_sum<16>(sum) / (float)BN;
+                    const float mean = group_sum<16>(sum) / (float)TN;
                     float m2 = 0.0f;
 #pragma unroll
                     for (int j = 0; j < FN; j++) {
@@ -1496,14 +1496,17 @@ hipError_t launch_tail(hipStream_t s, const GemmArgs &g, EpiArgs ep, const TailP
     return hipGetLastError();
 }
 
-// The in-workgroup split-K Residual GEMM (gemm_kgroup_kernel, 64 x 48 tiles,
-// 4 K groups of 2 waves): taken for M <= 1024, K <= 1024 (the out-projection
-// at 865 tokens: 15.6 us as the balanced tail's 504 pieces), when N % 48 == 0
-// and each group has at least two whole 32-wide slices.
+// The in-workgroup split-K Residual GEMM (gemm_kgroup_kernel, 32 x 96 tiles,
+// 2 K groups of 2 x 2 waves): taken for M <= 1024, K <= 1024 (the out-
+// projection at 865 tokens: 15.6 us as the balanced tail's 504 pieces), when
+// N % 96 == 0 and each group has at least two whole 32-wide slices.  A sweep
+// of tiles, wave shapes and group counts at 865 x 768 x 768 (lab, 200-launch
+// bursts): 13.3 us here, 13.7 for 32 x 48 with two groups of 2 x 1, 15.0 for
+// 64 x 48 with four groups of 2 x 1, 15.9 for 64 x 64 with two groups.
 // VESTRA_HIP_GEMM_KGROUP=0 never takes it, =1 whenever the shape allows.
 bool use_kgroup(const GemmArgs &g) {
-    constexpr size_t KG = 4, BK = 32;
-    if (g.n % 48 != 0 || g.k % (KG * BK) != 0 || g.k / KG < 2 * BK || g.m > INT32_MAX) return false;
+    constexpr size_t KG = 2, BK = 32;
+    if (g.n % 96 != 0 || g.k % (KG * BK) != 0 || g.k / KG < 2 * BK || g.m > INT32_MAX) return false;
     const char *env = std::getenv("VESTRA_HIP_GEMM_KGROUP");  // per call (tests switch it)
     if (env && env[0] == '0') return false;
     if (env && env[0] == '1') return true;
@@ -1511,14 +1514,14 @@ bool use_kgroup(const GemmArgs &g) {
 }
 
 hipError_t launch_kgroup(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
-    constexpr int BM = 64, BN = 48, BK = 32, WM = 2, WN = 1, KG = 4;
+    constexpr int BM = 32, BN = 96, BK = 32, WM = 2, WN = 2, KG = 2;
     constexpr size_t lds = (size_t)KG * 2 * (BM + BN) * BK * sizeof(float);
     auto kernel = gemm_kgroup_kernel<BM, BN, BK, WM, WN, KG>;
     static std::atomic<uint64_t> configured{0};
     if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
     if (g.stats_out) {
         ep.stats_out = reinterpret_cast<float2 *>(g.stats_out);
-        ep.stats_chunks = (int)(g.n / BN);
+        ep.stats_chunks = (int)(g.n / (BN / WN));
         if (g.stats_out_chunks) *g.stats_out_chunks = ep.stats_chunks;
     }
     dim3 grid((unsigned)(g.n / BN), (unsigned)((g.m + BM - 1) / BM));
