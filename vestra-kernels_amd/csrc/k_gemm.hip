@@ -1402,13 +1402,13 @@ void default_tile(const GemmArgs &g, Tile *t, int *splits) {
             *t = Tile{64, 128, 64, 2, 4};
         }
     } else {
-        if (narrow && long_k) {
-            *t = Tile{128, 128, 32, 2, 4};
-            *splits = 3;
-        } else {
-            // QKV at 4 x 865 tokens: 107.1 us against 108.8 for 128 x 128 x 32.
-            *t = Tile{64, 64, 32, 2, 2};
-        }
+        // QKV at 4 x 865 tokens: 107.1 us against 108.8 for 128 x 128 x 32.
+        // fc2 (narrow, long K) at 4 x 865 tokens: 132.7 us unsplit (with the
+        // balanced tail for its last round) against 137.3 for 128 x 128 x 32
+        // split-K 3 with its reduction, and its Residual epilogue then writes
+        // the row statistics the next layer's QKV takes (the 12-layer
+        // encoder 6.51 -> 6.37 ms).
+        *t = Tile{64, 64, 32, 2, 2};
     }
 }
 
