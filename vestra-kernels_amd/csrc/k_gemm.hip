@@ -33,12 +33,18 @@
 //     rstd * (x . W'^T - mean * c) + b',   W' = W diag(g),
 //     c[n] = sum_k W'[n][k],               b' = b + W . be,
 // on the raw rows x (W', c and b' prepared once).  Every workgroup sees
-// whole rows of A (K is not split), so the row statistics come from the A
-// slices as they pass through registers on their way to LDS: each thread
-// sums (x - s) and (x - s)^2 over its chunks, with s = x[row][0] as a shift
-// that keeps the variance free of cancellation, and the threads of a row
-// reduce once after the slice loop.  Balanced-tail pieces publish their
-// sums beside their partial tiles; the last piece adds them in piece order.
+// whole rows of A (K is not split), so the row statistics come either from
+// the producer of x (LNF == 2: per-chunk mean and M2, merged with Chan's
+// formula) or from the A slices as they pass through registers on their way
+// to LDS (LNF == 1): each thread sums (x - s) and (x - s)^2 over its chunks,
+// with s the mean of the row's first slice, and the threads of a row reduce
+// once after the slice loop.  Balanced-tail pieces publish their sums beside
+// their partial tiles; the last piece adds them in piece order.  The GEMM
+// term x . W'^T - mean * c cancels in proportion to |mean| / std, as the
+// crate's own float32 LayerNorm sums do (scalar::layernorm sums the raw row
+// in float32 too); staging x - s instead costs fc1 about 1 us per block on
+// gfx950, because the subtraction pulls the wait for the next slice's loads
+// ahead of the slice's last MFMAs.
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
@@ -276,6 +282,34 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     // load is writing (and need no wait of their own); otherwise one set.
     constexpr bool LN_LOOP = LNF == 1;  // row sums taken from the A slices
     constexpr bool LN_ANY = LNF != 0;
+    // LayerNorm fold, statistics from the A slices (LNF == 1): this thread's
+    // A chunks c = tid + i * NT all lie in row c / CPR of the tile (NT is a
+    // multiple of CPR); ln_s1 / ln_s2 sum x - s and (x - s)^2 over the chunks
+    // it sees, with s = ln_sh[i] the mean of the row's first BK elements.
+    // Then (s - mean)^2 <= M2 / BK, so S2 = M2 + K (s - mean)^2 stays within
+    // (1 + K / BK) M2 whatever the row holds, and S2 / K - (S1 / K)^2 does not
+    // cancel (a shift by one element does: x[row][0] far from the mean).
+    // The CPR threads of a row hold those BK elements between them (chunk
+    // tid % CPR of slice 0), loaded here and summed after the first slice is
+    // stored.  Every piece of a balanced-tail tile derives the same shift
+    // from the same loads, so their partial sums add.
+    constexpr int LA = LN_LOOP ? ACH : 1;
+    float ln_sh[LA], ln_s1[LA], ln_s2[LA];
+    f32x4 ln_first[LA];
+    if constexpr (LN_ANY) {
+        static_assert(EXACT && !SPLIT && CONV == 0 && (EPI == Epi::Gelu || EPI == Epi::Qkv),
+                      "LayerNorm fold: whole-slice Gelu / Qkv GEMMs");
+        static_assert(NT % CPR == 0, "a thread's chunks share one row");
+    }
+    if constexpr (LN_LOOP) {
+#pragma unroll
+        for (int i = 0; i < ACH; i++) {
+            ln_first[i] = *reinterpret_cast<const f32x4 *>(A + (size_t)min(m0 + (tid + i * NT) / CPR, M - 1) * K +
+                                                            (tid % CPR) * 4);
+            ln_s1[i] = 0.0f;
+            ln_s2[i] = 0.0f;
+        }
+    }
     f32x4 ra_sets[LN_LOOP ? 2 : 1][ACH], rb[BCH];
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
@@ -381,23 +415,6 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
         }
     };
 
-    // LayerNorm fold: this thread's A chunks c = tid + i * NT all lie in row
-    // c / CPR of the tile (NT is a multiple of CPR); ln_sh[i] is that row's
-    // first element, ln_s1 / ln_s2 the shifted sums over the chunks seen.
-    constexpr int LA = LN_LOOP ? ACH : 1;
-    float ln_sh[LA], ln_s1[LA], ln_s2[LA];
-    if constexpr (LN_ANY)
-        static_assert(EXACT && !SPLIT && CONV == 0 && (EPI == Epi::Gelu || EPI == Epi::Qkv),
-                      "LayerNorm fold: whole-slice Gelu / Qkv GEMMs");
-    if constexpr (LN_LOOP) {
-        static_assert(NT % CPR == 0, "a thread's chunks share one row");
-#pragma unroll
-        for (int i = 0; i < ACH; i++) {
-            ln_sh[i] = A[(size_t)min(m0 + (tid + i * NT) / CPR, M - 1) * K];
-            ln_s1[i] = 0.0f;
-            ln_s2[i] = 0.0f;
-        }
-    }
     // LNF == 2: the producer's statistics of this tile's rows, one (mean,
     // M2) per 32-column chunk of the row (stats_chunks per row), prefetched
     // before the slice loop: TPR threads per row, ln_cpt chunks each (host:
@@ -474,6 +491,14 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     gload(kbeg, P0{});
     lstore(0, P0{});
     __syncthreads();
+    if constexpr (LN_LOOP) {
+        // After the first slice's stores, so that they do not wait for it.
+#pragma unroll
+        for (int i = 0; i < ACH; i++) {
+            const float part = (ln_first[i][0] + ln_first[i][1]) + (ln_first[i][2] + ln_first[i][3]);
+            ln_sh[i] = group_sum<CPR>(part) * (1.0f / BK);
+        }
+    }
     if constexpr (EXACT) {
         // Branch-free slice loop: the last iteration reloads its own slice
         // into the idle buffer (never read again), so each iteration is one
