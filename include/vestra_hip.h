@@ -144,10 +144,13 @@ vh_status vh_flash_attention_f32_da3_base(const vh_runtime *rt, const vh_tensor 
  * above).  The key-split partials live in a 64 MiB device array of the
  * library, one per GPU, reserved until the process ends; heads*tokens above
  * 63550 is rejected with VH_ERR_KERNEL before any launch.  Every call on a
- * GPU shares that GPU's array: calls ordered on one stream are safe, calls
- * that overlap on one GPU (runtimes on different streams, host threads
- * without ordering) race.  Results are bit-identical to the allocating entry
- * point's. */
+ * GPU shares that GPU's array, and the library orders the calls in the order
+ * they are made: each launch waits (hipStreamWaitEvent) for the previous
+ * call's launch, on whatever runtime or stream it ran, so runtimes on
+ * different streams and host threads may call it freely.  Under stream
+ * capture that wait is not recorded: replays of such a graph are ordered
+ * only by the caller against other uses of the array.  Results are
+ * bit-identical to the allocating entry point's. */
 vh_status vh_flash_attention_f32_da3_base_into(const vh_runtime *rt, const vh_tensor *q,
                                                const vh_tensor *k, const vh_tensor *v,
                                                size_t heads, size_t tokens, int token_major,

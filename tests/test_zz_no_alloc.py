@@ -52,3 +52,25 @@ def test_no_alloc_attention_rejects_before_launch(rt):
     rt.flash_attention_f32_da3_base_into(q, k, v, 1, MAX_ROWS, False, out)
     exp = rt.download_f32(rt.flash_attention_f32_da3_base(q, k, v, 1, MAX_ROWS, False))
     assert_bits_equal(rt.download_f32(out), exp, "no-alloc attention at the limit")
+
+
+def test_no_alloc_attention_two_runtimes_back_to_back(rt):
+    """Two runtimes (two streams) share the GPU's scratch array: each call
+    waits for the previous call's launch, so back-to-back calls without a
+    host synchronisation between them give the allocating entry point's bits
+    (12 x 865 and 8 x 865 both split the keys across workgroups, so both
+    launches write partials)."""
+    other = vh.Runtime(0)
+    cases = ((rt, 12, 865, 50), (other, 8, 865, 60), (rt, 12, 865, 70), (other, 3, 600, 80))
+    inputs, outs, exps = [], [], []
+    for r, heads, tokens, seed in cases:
+        q, k, v = _qkv(r, heads, tokens, seed)
+        inputs.append((q, k, v))
+        exps.append(r.download_f32(r.flash_attention_f32_da3_base(q, k, v, heads, tokens, True)))
+        outs.append(r.alloc_f32(heads * tokens * 64))
+    rt.synchronize()
+    other.synchronize()
+    for (r, heads, tokens, _), (q, k, v), out in zip(cases, inputs, outs):
+        r.flash_attention_f32_da3_base_into(q, k, v, heads, tokens, True, out)
+    for (r, heads, tokens, _), out, exp in zip(cases, outs, exps):
+        assert_bits_equal(r.download_f32(out), exp, f"no-alloc attention {heads}x{tokens} on two streams")

@@ -671,10 +671,15 @@ static __device__ __align__(256) float scratch[kScratchFloats];
 namespace {
 
 constexpr int kMaxScratchDevices = 64;
-std::mutex g_scratch_mu;
+std::mutex g_scratch_mu;  // guards the slots and orders the uses of each array
 float *g_scratch_ptr[kMaxScratchDevices] = {};
+// Per device, an event recorded after the last launch that used its array,
+// on whichever stream it ran: the next use, from any stream, waits for it.
+// Created with the slot, never destroyed (the array also lives until exit).
+hipEvent_t g_scratch_done[kMaxScratchDevices] = {};
 
-// With `device` current: its address of `scratch`, looked up once.
+// With `device` current: its address of `scratch` and its last-use event,
+// set up once.
 vh_status scratch_init(int device, float **out) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (device < 0 || device >= kMaxScratchDevices)
@@ -684,6 +689,10 @@ vh_status scratch_init(int device, float **out) {
         hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !p)
             return fail(VH_ERR_INITIALIZE, hip_msg("scratch symbol address", e));
+        hipEvent_t ev = nullptr;
+        e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e != hipSuccess) return fail(VH_ERR_INITIALIZE, hip_msg("scratch event", e));
+        g_scratch_done[device] = ev;
         g_scratch_ptr[device] = static_cast<float *>(p);
     }
     *out = g_scratch_ptr[device];
@@ -1174,10 +1183,23 @@ extern "C" vh_status vh_flash_attention_f32_da3_base_into(const vh_runtime *rt,
     RtState &s = *rt->s;
     TRY(set_device(s));
     if (!s.scratch) return fail(VH_ERR_INITIALIZE, std::string(what) + ": no scratch on this device");
-    hipError_t e = vh::launch_flash_attention(s.stream, q->ptr, k->ptr, v->ptr, out->ptr, heads,
-                                              tokens, heads, token_major != 0, s.scratch,
-                                              kScratchFloats);
+    // One use of the device's array at a time, in call order: this stream
+    // waits for the last use (on any stream), and this launch becomes the
+    // last use.  Under stream capture the graph's own order applies instead
+    // (an event recorded outside a capture cannot be waited on inside it).
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    const hipEvent_t done = g_scratch_done[s.device];
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(s.stream, &capture);
     if (e != hipSuccess) return fail(VH_ERR_KERNEL, hip_msg(what, e));
+    const bool order = capture == hipStreamCaptureStatusNone;
+    if (order && (e = hipStreamWaitEvent(s.stream, done, 0)) != hipSuccess)
+        return fail(VH_ERR_KERNEL, hip_msg(what, e));
+    e = vh::launch_flash_attention(s.stream, q->ptr, k->ptr, v->ptr, out->ptr, heads, tokens, heads,
+                                   token_major != 0, s.scratch, kScratchFloats);
+    if (e != hipSuccess) return fail(VH_ERR_KERNEL, hip_msg(what, e));
+    if (order && (e = hipEventRecord(done, s.stream)) != hipSuccess)
+        return fail(VH_ERR_KERNEL, hip_msg(what, e));
     return VH_OK;
     GUARD_END
 }
