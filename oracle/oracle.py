@@ -15,7 +15,9 @@ from pathlib import Path
 import numpy as np
 
 _HERE = Path(__file__).resolve().parent
-_LIB_PATH = _HERE / "libvk_oracle.so"
+# VKO_ORACLE_LIB selects another build of the same sources (the sanitizer
+# build of `make -C oracle asan`); the default is the plain build.
+_LIB_PATH = Path(os.environ.get("VKO_ORACLE_LIB") or _HERE / "libvk_oracle.so")
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i64p = ctypes.POINTER(ctypes.c_int64)

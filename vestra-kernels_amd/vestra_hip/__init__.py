@@ -10,6 +10,7 @@ missing, importing ``lib()`` raises.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import numpy as np
@@ -17,7 +18,9 @@ import numpy as np
 from . import da3, seeded  # noqa: F401  (re-exported helpers)
 
 _HERE = Path(__file__).resolve().parent
-LIB_PATH = _HERE / "libvestra_hip.so"
+# VESTRA_HIP_LIB selects another build of the same sources (the host-side
+# sanitizer build of `make -C vestra-kernels_amd asan`, for CPU-only runs).
+LIB_PATH = Path(os.environ.get("VESTRA_HIP_LIB") or _HERE / "libvestra_hip.so")
 
 _p = ctypes.c_void_p
 _sz = ctypes.c_size_t
