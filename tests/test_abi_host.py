@@ -40,23 +40,86 @@ RUST_BINDING = ROOT / "vestra-kernels_amd" / "rust" / "hip.rs"
 RUST_UNBOUND = {"vh_runtime_clone", "vh_tensor_is_empty"}
 
 
+C_BASE_TO_RUST = {"size_t": "usize", "int": "c_int", "float": "f32", "int64_t": "i64",
+                  "void": "c_void", "char": "c_char", "vh_status": "Status"}
+
+
+def _rust_name(c_base):
+    """vh_q8_tensor -> VhQ8Tensor; the scalar types through C_BASE_TO_RUST."""
+    if c_base in C_BASE_TO_RUST:
+        return C_BASE_TO_RUST[c_base]
+    assert c_base.startswith("vh_"), c_base
+    return "".join(w[:1].upper() + w[1:] for w in c_base.split("_"))
+
+
+def c_type_as_rust(decl, has_name=True):
+    """The Rust FFI spelling of a C parameter or return type: `const T *p`
+    -> `*const T`, `T **p` -> `*mut *mut T`, `const T *const *p` ->
+    `*const *const T`, built from the innermost pointee outwards (each
+    level's const qualifier decides the next pointer's mutability)."""
+    decl = " ".join(decl.replace("*", " * ").split())
+    tokens = decl.split()
+    if has_name:
+        tokens = tokens[:-1]  # the parameter name
+    parts = " ".join(tokens).split("*")
+    base_words = parts[0].split()
+    const = "const" in base_words
+    base = [w for w in base_words if w != "const"]
+    assert len(base) == 1, decl
+    rust = _rust_name(base[0])
+    for qual in parts[1:]:
+        rust = ("*const " if const else "*mut ") + rust
+        const = "const" in qual.split()
+    return rust
+
+
 def test_rust_binding_declares_the_header():
     """The `hip` feature's FFI block (rust/hip.rs) declares every C-ABI
-    function with the header's parameter count (it is compiled by the
-    crate's build, not here)."""
+    function with the header's parameter and return types, in order
+    (size_t -> usize, int -> c_int, float -> f32, int64_t -> i64,
+    `const T *` -> `*const T`, `T *` / `T **` -> `*mut ...`).  The Rust file
+    is compiled by the crate's build, not here: no Rust toolchain in this
+    image."""
     text = RUST_BINDING.read_text()
     block = text[text.index('unsafe extern "C" {'):]
     block = block[:block.index("\n}\n")]
-    rust = dict(re.findall(r"fn (vh_[a-z0-9_]+)\(([^)]*)\)", block, flags=re.S))
+    rust = {m.group(1): (m.group(2), (m.group(3) or "").strip())
+            for m in re.finditer(r"fn (vh_[a-z0-9_]+)\(([^)]*)\)\s*(?:->\s*([^;]+))?;", block, flags=re.S)}
     names = set(declared_functions())
     assert set(rust) == names - RUST_UNBOUND, set(rust) ^ (names - RUST_UNBOUND)
     header = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    for name, params in rust.items():
-        c_params = re.search(name + r"\s*\(([^)]*)\)", header).group(1)
-        n_c = 0 if c_params.strip() in ("", "void") else c_params.count(",") + 1
-        n_r = 0 if not params.strip() else params.count(",") + 1
-        assert n_c == n_r, (name, n_c, n_r)
+    checked = 0
+    for name, (params, ret) in rust.items():
+        m = re.search(r"([A-Za-z_][\w\s\*]*?)\b" + name + r"\s*\(([^)]*)\)", header)
+        c_ret, c_params = m.group(1), m.group(2)
+        c_list = [] if c_params.strip() in ("", "void") else [p.strip() for p in c_params.split(",")]
+        r_list = [p.strip() for p in params.split(",") if p.strip()]
+        assert len(c_list) == len(r_list), (name, c_list, r_list)
+        for c_p, r_p in zip(c_list, r_list):
+            r_type = " ".join(r_p.split(":", 1)[1].split())
+            assert c_type_as_rust(c_p) == r_type, (name, c_p, r_p)
+            checked += 1
+        c_ret = c_ret.strip()
+        want = "" if c_ret == "void" else c_type_as_rust(c_ret, has_name=False)
+        assert " ".join(ret.split()) == want, (name, c_ret, ret)
+    assert checked > 250
     assert 'compile_error!("features `cuda` and `hip` are exclusive' in text
+
+
+def test_rust_type_mapping_catches_mismatches():
+    """The mapping the binding test uses distinguishes what an FFI mistake
+    would confuse."""
+    assert c_type_as_rust("size_t n") == "usize"
+    assert c_type_as_rust("int flag") == "c_int"
+    assert c_type_as_rust("float eps") == "f32"
+    assert c_type_as_rust("const float *x") == "*const f32"
+    assert c_type_as_rust("float *x") == "*mut f32"
+    assert c_type_as_rust("const int64_t *pos") == "*const i64"
+    assert c_type_as_rust("vh_tensor **out") == "*mut *mut VhTensor"
+    assert c_type_as_rust("const vh_block *const *blocks") == "*const *const VhBlock"
+    assert c_type_as_rust("const vh_q8_tensor *q") == "*const VhQ8Tensor"
+    assert c_type_as_rust("vh_status", has_name=False) == "Status"
+    assert c_type_as_rust("const char *", has_name=False) == "*const c_char"
 
 
 def test_null_handles_fail_before_any_device_call():
