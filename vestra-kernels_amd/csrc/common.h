@@ -85,6 +85,17 @@ __device__ __forceinline__ T load_or(const T *p, const T *alt, size_t i, T fallb
 // stores that follow need no waits between them (vmcnt counts stores too).
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
+// Non-temporal store for the Store, GELU and Residual GEMM epilogues: the
+// lines are not left dirty in the XCD's L2, so the end-of-kernel write-back
+// that makes them visible to the next kernel has less to do (Q8_0 GEMM at
+// the fc1 shape 15.5 -> 14.5 us, the f32 block's QKV-less GEMMs 0.4-0.5 us
+// each).  Head-major Q/K/V stay cached: the attention re-reads each K and V
+// panel from every query tile, and streamed Q/K/V cost it 0.5 us.
+template <typename T>
+__device__ __forceinline__ void stream_store(T *p, T v) {
+    __builtin_nontemporal_store(v, p);
+}
+
 // One DPP lane permutation (a VALU modifier, no LDS round trip).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {

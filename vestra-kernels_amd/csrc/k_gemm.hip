@@ -929,13 +929,13 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                             v = add_rn(v, bias[j]);
                         if constexpr (EPI == Epi::Store) {
                             if (ep.gamma) v = mul_rn(v, gamma[j]);
-                            ep.c[idx] = v;
+                            stream_store(ep.c + idx, v);
                         } else if constexpr (EPI == Epi::Gelu) {
-                            ep.c[idx] = gelu_fast_form(v);
+                            stream_store(ep.c + idx, gelu_fast_form(v));
                         } else {
                             if (ep.gamma) v = mul_rn(v, gamma[j]);
                             const float o = add_rn(resid[i][j][r], v);
-                            ep.c[idx] = o;
+                            stream_store(ep.c + idx, o);
                             if constexpr (EPI == Epi::Residual) outv[i][j][r] = o;
                         }
                     }
@@ -1167,7 +1167,7 @@ __global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kgroup_kernel(const floa
                 const float o = add_rn(resid[i][j][r], v);
                 outv[i][j][r] = o;
                 const int row = rbase + i * 16 + r, col = cbase + j * 16;
-                if (row < M && col < N) ep.c[(size_t)row * N + col] = o;
+                if (row < M && col < N) stream_store(ep.c + (size_t)row * N + col, o);
             }
     {
         // The 16 lanes of a lane group hold a row's TN values of this wave

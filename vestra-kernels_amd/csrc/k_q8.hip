@@ -559,7 +559,7 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(const int8_t *__restrict
                         if (ep.gamma) v = mul_rn(v, gamma[j]);
                         if constexpr (EPI == Epi::Residual) v = add_rn(resid[i][j][r], v);
                     }
-                    row_ptr(i, j, r)[loff] = v;
+                    stream_store(row_ptr(i, j, r) + loff, v);
                 }
         return;
     }
