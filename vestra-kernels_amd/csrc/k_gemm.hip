@@ -1522,12 +1522,16 @@ hipError_t launch_tail(hipStream_t s, const GemmArgs &g, EpiArgs ep, const TailP
 }
 
 // The in-workgroup split-K Residual GEMM (gemm_kgroup_kernel, 32 x 96 tiles,
-// 2 K groups of 2 x 2 waves): taken for M <= 1024, K <= 1024 (the out-
+// 2 K groups of 2 x 2 waves, 64-wide k-slices when each group has at least
+// two of them, else 32-wide): taken for M <= 1024, K <= 1024 (the out-
 // projection at 865 tokens: 15.6 us as the balanced tail's 504 pieces), when
 // N % 96 == 0 and each group has at least two whole 32-wide slices.  A sweep
 // of tiles, wave shapes and group counts at 865 x 768 x 768 (lab, 200-launch
-// bursts): 13.3 us here, 13.7 for 32 x 48 with two groups of 2 x 1, 15.0 for
-// 64 x 48 with four groups of 2 x 1, 15.9 for 64 x 64 with two groups.
+// bursts): 13.3 us here with 32-wide slices, 13.7 for 32 x 48 with two
+// groups of 2 x 1, 15.0 for 64 x 48 with four groups of 2 x 1, 15.9 for
+// 64 x 64 with two groups.  In the block (per-launch events, two alternating
+// runs): 32-wide slices 17.3 us, three K groups 16.7, four 16.8, 64-wide
+// slices (half the barriers) 16.6-16.7.
 // VESTRA_HIP_GEMM_KGROUP=0 never takes it, =1 whenever the shape allows.
 bool use_kgroup(const GemmArgs &g) {
     constexpr size_t KG = 2, BK = 32;
@@ -1538,8 +1542,8 @@ bool use_kgroup(const GemmArgs &g) {
     return g.m <= 1024 && g.k <= 1024;
 }
 
-hipError_t launch_kgroup(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
-    constexpr int BM = 32, BN = 96, BK = 32, WM = 2, WN = 2, KG = 2;
+template <int BM, int BN, int BK, int WM, int WN, int KG>
+hipError_t launch_kgroup_t(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     constexpr size_t lds = (size_t)KG * 2 * (BM + BN) * BK * sizeof(float);
     auto kernel = gemm_kgroup_kernel<BM, BN, BK, WM, WN, KG>;
     static std::atomic<uint64_t> configured{0};
@@ -1552,6 +1556,11 @@ hipError_t launch_kgroup(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     dim3 grid((unsigned)(g.n / BN), (unsigned)((g.m + BM - 1) / BM));
     kernel<<<grid, WM * WN * KG * 64, lds, s>>>(g.a, g.bt, (int)g.m, (int)g.n, (int)g.k, ep);
     return hipGetLastError();
+}
+
+hipError_t launch_kgroup(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
+    if (g.k % (2 * 64) == 0 && g.k / 2 >= 2 * 64) return launch_kgroup_t<32, 96, 64, 2, 2, 2>(s, g, ep);
+    return launch_kgroup_t<32, 96, 32, 2, 2, 2>(s, g, ep);
 }
 
 // LayerNorm-folded Gelu / Qkv GEMM (ln_fold_c set): whole slices and no K
