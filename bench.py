@@ -100,6 +100,32 @@ def measured_traffic(launch: str):
 
 
 MFMA_SUMMARY = ROOT / "profiles" / "block_865_mfma_busy.md"
+TRACE_SUMMARY = ROOT / "profiles" / "block_865_kernel_trace.md"
+
+
+def measured_trace_us() -> dict:
+    """Per-launch kernel-trace durations of one block at 865 tokens from the
+    committed rocprofv3 --kernel-trace summary (median per kernel, summed over
+    the kernels of a launch), keyed by launch name; {} when absent.  Unlike
+    the per-launch HIP events, the trace adds no event packets around each
+    launch."""
+    try:
+        text = TRACE_SUMMARY.read_text()
+    except OSError:
+        return {}
+    out = {}
+    in_block = False
+    for line in text.splitlines():
+        if line.startswith("## One f32 block"):
+            in_block = True
+            continue
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if in_block and len(cells) == 3 and cells[0].startswith("`"):
+            try:
+                out[cells[0].strip("`")] = out.get(cells[0].strip("`"), 0.0) + float(cells[2])
+            except ValueError:
+                pass
+    return out
 
 
 def measured_mfma_busy() -> dict:
@@ -842,6 +868,17 @@ def main() -> int:
     if mfma:
         result["mfma_busy_source"] = ("profiles/block_865_mfma_busy.md: committed rocprofv3 "
                                       "--pmc summary, not measured in this run")
+    trace = measured_trace_us()
+    for name, us in trace.items():
+        if name in ker and name in FLOPS:
+            ker[name]["trace_us"] = round(us, 2)
+            ker[name]["frac_fp32_mfma_trace"] = round(FLOPS[name] / (us * 1e-6) / 1e12 /
+                                                     PEAK_FP32_MFMA_TFLOPS, 4)
+    if trace:
+        result["trace_source"] = ("profiles/block_865_kernel_trace.md: committed rocprofv3 "
+                                  "--kernel-trace summary (medians over its block launches), not "
+                                  "measured in this run; avg_us and frac_fp32_mfma are this run's "
+                                  "per-launch HIP events, which add 1-2.5 us per launch")
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_block(args.cpu_seconds)
         cpu_k = cpu_kernels()
