@@ -335,6 +335,32 @@ def test_kgroup_residual_gemm(rt, monkeypatch, m, k, mode):
     assert (got.view(np.uint32) != other.view(np.uint32)).any()
 
 
+@pytest.mark.parametrize("m,k,mode", [(865, 768, "default"), (97, 768, "default"),
+                                      (865, 3072, "forced")])
+def test_kgroup_store_gemm(rt, monkeypatch, m, k, mode):
+    """The Store epilogue ((acc + b) * LayerScale, CudaLinearF32::run) on the
+    K-group GEMM, the default for the out-projection's shape: within 1e-5 of
+    the oracle, identical run to run, and different in some bits from
+    unsplit 64 x 64 tiles (so the kernel ran)."""
+    n = 768
+    a = seeded.normal(81 + m, m * k)
+    w = seeded.normal(82, k * n, 0.02)
+    bias = seeded.normal(83, n, 0.02)
+    ls = (0.1 + 0.9 * seeded.uniform01(85, n)).astype(np.float32)
+    lin = rt.prepare_linear_f32(k, n, w, bias, ls)
+    at = rt.upload_f32(a)
+    monkeypatch.setenv("VESTRA_HIP_GEMM_KGROUP", "1" if mode == "forced" else "")
+    got = rt.download_f32(lin.run(at, m))
+    assert_bits_equal(rt.download_f32(lin.run(at, m)), got, "kgroup store rerun")
+    assert max_rel(got, O.linear_bias_scale(a, w, bias, ls, m, n, k)) <= 1e-5
+    monkeypatch.setenv("VESTRA_HIP_GEMM_KGROUP", "0")
+    monkeypatch.setenv("VESTRA_HIP_GEMM_TAIL", "0")
+    monkeypatch.setenv("VESTRA_HIP_GEMM_TILE", "64x64x32x2x2x1")
+    other = rt.download_f32(lin.run(at, m))
+    assert max_rel(got, other) <= 1e-5
+    assert (got.view(np.uint32) != other.view(np.uint32)).any()
+
+
 @pytest.mark.parametrize("images, rows, cols, rope", [
     (1, 24, 36, False), (1, 24, 36, True), (4, 24, 36, True), (1, 48, 72, True)],
     ids=["865", "865-rope", "4x865-rope", "3457-rope"])

@@ -969,8 +969,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     }
 }
 
-// Residual GEMM with the K split inside the workgroup, for the narrow short-K
-// projection (the out-projection: 865 x 768 x 768, whose 64 x 64 tiles are
+// Residual (or Store) GEMM with the K split inside the workgroup, for the
+// narrow short-K projection (the out-projection: 865 x 768 x 768, whose 64 x 64 tiles are
 // fewer than the CUs).  KG groups of WM x WN waves share a BM x BN tile;
 // group g runs K range [g K / KG, (g + 1) K / KG) through its own double-
 // buffered LDS stages (the slice layout and fragment schedule of
@@ -982,7 +982,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
 // per CU, two waves per SIMD, with no partial tiles leaving the CU and no
 // second launch.  With ep.stats_out, group 0 also writes each row's (mean,
 // M2) over each wave's TN columns: one chunk per wave column.
-template <int BM, int BN, int BK, int WM, int WN, int KG>
+template <int BM, int BN, int BK, int WM, int WN, int KG, Epi EPI = Epi::Residual>
 __global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kgroup_kernel(const float *__restrict__ A,
                                                                       const float *__restrict__ Bt,
                                                                       int M, int N, int K, EpiArgs ep) {
@@ -1035,6 +1035,7 @@ __global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kgroup_kernel(const floa
     const int rbase = m0 + wm * TM + 4 * lh;
     const int cbase = n0 + wn * TN + li;
     float bias[FN], gamma[FN], resid[FM][FN][4];
+    static_assert(EPI == Epi::Residual || EPI == Epi::Store, "K-group epilogues: Residual and Store");
     // The epilogue's reads (group 0): bias, LayerScale and the residual tile.
     auto epi_loads = [&]() {
 #pragma unroll
@@ -1043,14 +1044,16 @@ __global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kgroup_kernel(const floa
             bias[j] = load_or(ep.bias, (const float *)ep.c, col, 0.0f);
             gamma[j] = load_or(ep.gamma, (const float *)ep.c, col, 1.0f);
         }
+        if constexpr (EPI == Epi::Residual) {
 #pragma unroll
-        for (int i = 0; i < FM; i++)
+            for (int i = 0; i < FM; i++)
 #pragma unroll
-            for (int j = 0; j < FN; j++)
+                for (int j = 0; j < FN; j++)
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    resid[i][j][r] =
-                        ep.c[(size_t)min(rbase + i * 16 + r, M - 1) * N + min(cbase + j * 16, N - 1)];
+                    for (int r = 0; r < 4; r++)
+                        resid[i][j][r] =
+                            ep.c[(size_t)min(rbase + i * 16 + r, M - 1) * N + min(cbase + j * 16, N - 1)];
+        }
     };
 
     f32x4 acc[FM][FN];
@@ -1164,7 +1167,7 @@ __global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kgroup_kernel(const floa
                 float v = acc[i][j][r];
                 if (ep.bias) v = add_rn(v, bias[j]);
                 if (ep.gamma) v = mul_rn(v, gamma[j]);
-                const float o = add_rn(resid[i][j][r], v);
+                const float o = EPI == Epi::Residual ? add_rn(resid[i][j][r], v) : v;
                 outv[i][j][r] = o;
                 const int row = rbase + i * 16 + r, col = cbase + j * 16;
                 if (row < M && col < N) stream_store(ep.c + (size_t)row * N + col, o);
@@ -1172,7 +1175,7 @@ __global__ __launch_bounds__(WM *WN *KG * 64) void gemm_kgroup_kernel(const floa
     {
         // The 16 lanes of a lane group hold a row's TN values of this wave
         // (FN per lane): mean and M2 over them by two 16-lane sums.
-        if (ep.stats_out) {
+        if (EPI == Epi::Residual && ep.stats_out) {
             const int chunk = (n0 + wn * TN) / TN;
 #pragma unroll
             for (int i = 0; i < FM; i++)
@@ -1521,9 +1524,9 @@ hipError_t launch_tail(hipStream_t s, const GemmArgs &g, EpiArgs ep, const TailP
     return hipGetLastError();
 }
 
-// The in-workgroup split-K Residual GEMM (gemm_kgroup_kernel, 32 x 96 tiles,
+// The in-workgroup split-K Residual and Store GEMM (gemm_kgroup_kernel, 32 x 96 tiles,
 // 2 K groups of 2 x 2 waves, 64-wide k-slices when each group has at least
-// two of them, else 32-wide): taken for M <= 1024, K <= 1024 (the out-
+// two of them, else 32-wide): taken for M, K, N <= 1024 (the out-
 // projection at 865 tokens: 15.6 us as the balanced tail's 504 pieces), when
 // N % 96 == 0 and each group has at least two whole 32-wide slices.  A sweep
 // of tiles, wave shapes and group counts at 865 x 768 x 768 (lab, 200-launch
@@ -1539,16 +1542,16 @@ bool use_kgroup(const GemmArgs &g) {
     const char *env = std::getenv("VESTRA_HIP_GEMM_KGROUP");  // per call (tests switch it)
     if (env && env[0] == '0') return false;
     if (env && env[0] == '1') return true;
-    return g.m <= 1024 && g.k <= 1024;
+    return g.m <= 1024 && g.k <= 1024 && g.n <= 1024;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int KG>
+template <Epi EPI, int BM, int BN, int BK, int WM, int WN, int KG>
 hipError_t launch_kgroup_t(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     constexpr size_t lds = (size_t)KG * 2 * (BM + BN) * BK * sizeof(float);
-    auto kernel = gemm_kgroup_kernel<BM, BN, BK, WM, WN, KG>;
+    auto kernel = gemm_kgroup_kernel<BM, BN, BK, WM, WN, KG, EPI>;
     static std::atomic<uint64_t> configured{0};
     if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
-    if (g.stats_out) {
+    if (EPI == Epi::Residual && g.stats_out) {
         ep.stats_out = reinterpret_cast<float2 *>(g.stats_out);
         ep.stats_chunks = (int)(g.n / (BN / WN));
         if (g.stats_out_chunks) *g.stats_out_chunks = ep.stats_chunks;
@@ -1558,9 +1561,10 @@ hipError_t launch_kgroup_t(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     return hipGetLastError();
 }
 
+template <Epi EPI>
 hipError_t launch_kgroup(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
-    if (g.k % (2 * 64) == 0 && g.k / 2 >= 2 * 64) return launch_kgroup_t<32, 96, 64, 2, 2, 2>(s, g, ep);
-    return launch_kgroup_t<32, 96, 32, 2, 2, 2>(s, g, ep);
+    if (g.k % (2 * 64) == 0 && g.k / 2 >= 2 * 64) return launch_kgroup_t<EPI, 32, 96, 64, 2, 2, 2>(s, g, ep);
+    return launch_kgroup_t<EPI, 32, 96, 32, 2, 2, 2>(s, g, ep);
 }
 
 // LayerNorm-folded Gelu / Qkv GEMM (ln_fold_c set): whole slices and no K
@@ -1627,7 +1631,13 @@ hipError_t dispatch(hipStream_t s, const GemmArgs &g, EpiArgs ep) {
     };
     if (g.stats_out_chunks) *g.stats_out_chunks = 0;
     if constexpr (EPI == Epi::Residual) {
-        if (!overridden && use_kgroup(g)) return launch_kgroup(s, g, ep);
+        if (!overridden && use_kgroup(g)) return launch_kgroup<EPI>(s, g, ep);
+    } else if constexpr (EPI == Epi::Store) {
+        // A Store GEMM keeps whole K per tile when the balanced tail is
+        // switched off (VESTRA_HIP_GEMM_TAIL=0: the summation order of an
+        // unsplit tile, which the direct convolution reproduces bit for bit).
+        const char *tail = std::getenv("VESTRA_HIP_GEMM_TAIL");
+        if (!overridden && !(tail && tail[0] == '0') && use_kgroup(g)) return launch_kgroup<EPI>(s, g, ep);
     }
     if constexpr (EPI != Epi::Qkv) {
         // Store, GELU and Residual: the last piece of a tail tile runs the
