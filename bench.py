@@ -233,7 +233,10 @@ class BlockBench:
         return out
 
 
-ENCODER_CASES = (("encoder_12x_4x865", 4, 24, 36), ("encoder_12x_1x3457", 1, 48, 72))
+# BASELINE config 5 (4 x 865 tokens, one 3457-token image) and the north
+# star's own target, one 504 x 336 image (865 tokens).
+ENCODER_CASES = (("encoder_12x_4x865", 4, 24, 36), ("encoder_12x_1x3457", 1, 48, 72),
+                 ("encoder_12x_1x865", 1, 24, 36))
 ENCODER_LAYERS = 12
 
 
@@ -258,8 +261,9 @@ def encoder_inputs(images: int, tokens: int):
 def gpu_encoder(reps: int = 5) -> dict:
     """the 12-layer DA3-BASE encoder (independent seeded
     layers) at 4 images x 865 tokens and at one 1008 x 672 image (3457
-    tokens), whole encoder between two HIP events, with its algorithmic
-    FLOPs as a fraction of the fp32-MFMA peak."""
+    tokens), and the north star's one 504 x 336 image (865 tokens), whole
+    encoder between two HIP events, with its algorithmic FLOPs as a
+    fraction of the fp32-MFMA peak."""
     import vestra_hip as vh
     from vestra_hip import da3
 
