@@ -215,13 +215,15 @@ def _assert_controls_fail(rt, ws, blocks, x, exp, images, T, pos, bar):
     assert max_rel(rt.download_f32(xt), exp) >= 10 * bar
 
 
-@pytest.mark.parametrize("images, rows, cols", [(4, 24, 36), (1, 48, 72)],
-                         ids=["config5a_4x865", "config5b_3457"])
+@pytest.mark.parametrize("images, rows, cols", [(4, 24, 36), (1, 48, 72), (1, 24, 36)],
+                         ids=["config5a_4x865", "config5b_3457", "north_star_1x865"])
 def test_encoder_12_layers_vs_oracle(rt, images, rows, cols):
     """the 12-layer encoder at 4 x 865 tokens (M = 3460)
     and at one 1008x672 image (48 x 72 grid + CLS = 3457 tokens; the CPU
     oracle takes the crate's generic attention path there, not the 865-token
-    flash gate), within 1e-3 of the oracle after all 12 layers.  LayerScale
+    flash gate), and the north star's own target, one 504 x 336 image (865
+    tokens, M <= 1024: the K-group out-projection and the 865-row tiles in
+    every layer), within 1e-3 of the oracle after all 12 layers.  LayerScale
     is drawn per channel from U(0.1, 1): every layer's branch then moves the
     residual stream by O(1) (the f32 oracle stays within 1.4e-6 of a float64
     transcription over 12 layers), so the bar checks each layer's GEMMs,
