@@ -76,6 +76,20 @@ TRAFFIC_SUMMARY = ROOT / "profiles" / "block_865_hbm_traffic.md"
 CLOCK_SETTLE_MS = 100.0
 
 
+def settle_clock(rt, fn, ms: float = CLOCK_SETTLE_MS) -> int:
+    """Untimed calls of fn for `ms` of wall time, synchronising every 20: the
+    host work between a section's cases idles the GPU, and its clock then
+    needs tens of ms of work to ramp back.  Returns the number of calls."""
+    rt.synchronize()
+    t0, n = time.perf_counter(), 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(20):
+            fn()
+        n += 20
+        rt.synchronize()
+    return n
+
+
 def pct_peak(kernels: dict) -> float:
     """GEMM + attention FLOPs of one block over the summed durations of those
     launches, as a percentage of the fp32-MFMA peak."""
@@ -337,9 +351,7 @@ def gpu_q8_0(steps: int) -> dict:
     x = rt.upload_f32(seeded.normal(11, m * k))
     w = seeded.normal(12, k * n, 0.02).reshape(k, n)
     wq = rt.quantize_q8_0(rt.upload_f32(np.ascontiguousarray(w.T).reshape(-1)), n, k)
-    for _ in range(3):
-        rt.gemm_q8_0(rt.quantize_q8_0(x, m, k), wq, m, n, k)
-    rt.synchronize()
+    settle_clock(rt, lambda: rt.gemm_q8_0(rt.quantize_q8_0(x, m, k), wq, m, n, k))
     rt.profile_reset()
     rt.profile_enable(True)
     keep = []  # outputs stay alive: no stream-ordered frees between the timed launches
@@ -358,9 +370,7 @@ def gpu_q8_0(steps: int) -> dict:
     # so its caches stay warm, and it is not the headline figure.
     aq = rt.quantize_q8_0(x, m, k)
     c = rt.upload_f32(np.zeros(m * n, np.float32))
-    for _ in range(3):
-        rt.gemm_q8_0_into(aq, wq, m, n, k, c)
-    rt.synchronize()
+    settle_clock(rt, lambda: rt.gemm_q8_0_into(aq, wq, m, n, k, c), CLOCK_SETTLE_MS / 4)
     rt.timer_start()
     for _ in range(steps):
         rt.gemm_q8_0_into(aq, wq, m, n, k, c)
@@ -398,7 +408,8 @@ def gpu_elementwise(reps: int = 20) -> dict:
     launches between two HIP events (`us_burst`, which can include host issue
     time for kernels shorter than one call's host cost) and per-launch event
     pairs (`us_event`, each carrying the events' own ~1-2 us).  Both are upper
-    bounds on the kernel's duration; `us` is the smaller."""
+    bounds on the kernel's duration; `us` is the smaller.  Each case first
+    runs for CLOCK_SETTLE_MS untimed, so that the clock has settled."""
     import vestra_hip as vh
     from vestra_hip import da3, seeded
 
@@ -454,9 +465,7 @@ def gpu_elementwise(reps: int = 20) -> dict:
     for label, cases in (("block_shapes", block_shapes), ("bandwidth_sizes", at_scale)):
         res = {}
         for name, fn, nbytes, prof_name in cases:
-            for _ in range(3):
-                fn()
-            rt.synchronize()
+            settle_clock(rt, fn)
             rt.timer_start()
             for _ in range(reps):
                 fn()  # an output dropped here is recycled by the stream-ordered pool
@@ -509,11 +518,12 @@ def gpu_dpt(reps: int = 20) -> dict:
                                          dpt_values(6, tc))
     rh, rw = 48, 72
     xr = rt.upload_f32(dpt_values(7, c * rh * rw))
-    for _ in range(3):
+    def step():
         conv.run(x, h, w)
         ct.run(xt, th, tw)
         rt.bilinear_resize_align_corners_f32(xr, c, rh, rw, 2 * rh, 2 * rw)
-    rt.synchronize()
+
+    settle_clock(rt, step)
     rt.profile_reset()
     rt.profile_enable(True)
     keep = []
@@ -585,8 +595,12 @@ def gpu_configs(reps: int = 20) -> dict:
     """BASELINE configs 1 and 2 standalone, each on its own stated inputs:
     the config-1 attention (token-major output [865, 768]) and the four
     config-2 projections with bias (vh_linear_run: one GEMM launch with the
-    bias epilogue).  Each case: a burst of `reps` launches between two HIP
-    events and per-launch event pairs; the smaller is reported."""
+    bias epilogue).  Each case first runs for CLOCK_SETTLE_MS untimed (the
+    preparation between cases idles the GPU and its clock drops), then
+    `reps` launches each between its own pair of HIP events (`us`, the
+    analogue of the reference's per-call timing, examples/
+    current_shape_bench.rs:24-40; events add 1-2.5 us per launch) and a burst
+    of `reps` back-to-back launches between two events (`us_burst`)."""
     import vestra_hip as vh
 
     rt = vh.Runtime(0)
@@ -605,9 +619,7 @@ def gpu_configs(reps: int = 20) -> dict:
                       2.0 * T * kk * nn))
     out = {}
     for label, fn, prof_name, flops in cases:
-        for _ in range(3):
-            fn()
-        rt.synchronize()
+        settle = settle_clock(rt, fn)
         rt.timer_start()
         for _ in range(reps):
             fn()
@@ -618,13 +630,15 @@ def gpu_configs(reps: int = 20) -> dict:
         prof = rt.profile_report()
         rt.profile_enable(False)
         del keep
-        us_event = 1e3 * prof[prof_name][1] / prof[prof_name][0]
-        us = min(us_burst, us_event)
+        us = 1e3 * prof[prof_name][1] / prof[prof_name][0]
         tf = flops / (us * 1e-6) / 1e12
-        out[label] = {"us": round(us, 2), "us_burst": round(us_burst, 2),
-                      "us_event": round(us_event, 2), "tflops": round(tf, 2),
-                      "frac_fp32_mfma": round(tf / PEAK_FP32_MFMA_TFLOPS, 4)}
-        log(f"  {label:34s} {us:8.2f} us {tf:7.2f} TF/s (burst {us_burst:.2f}, events {us_event:.2f})")
+        tf_burst = flops / (us_burst * 1e-6) / 1e12
+        out[label] = {"us": round(us, 2), "us_source": "per-launch HIP events",
+                      "tflops": round(tf, 2), "frac_fp32_mfma": round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
+                      "us_burst": round(us_burst, 2),
+                      "frac_fp32_mfma_burst": round(tf_burst / PEAK_FP32_MFMA_TFLOPS, 4),
+                      "clock_settle": {"ms": CLOCK_SETTLE_MS, "launches": settle}}
+        log(f"  {label:34s} {us:8.2f} us {tf:7.2f} TF/s per-launch events (burst {us_burst:.2f})")
     return out
 
 
