@@ -722,8 +722,13 @@ def cpu_kernels() -> dict:
 
 
 def cpu_dpt_conv(budget_s: float) -> dict:
-    """The oracle's direct conv2d (the crate's conv2d_naive restated, all
-    OpenMP threads) on the bench's 3x3 convolution shape."""
+    """The crate's CPU route for the bench's 3x3 convolution: Winograd
+    F(2x2, 3x3) with the AVX-512 product (conv::conv3x3_winograd_f2_prepared,
+    src/conv.rs:282-302 and 681-829; src/specialized.rs:597-633), the filter
+    prepared once as the DPT head prepares it, at 16 threads (`value`) and at
+    every core of the affinity mask, median of >= 10 warm runs.  The direct
+    conv2d_naive (the definition the crate tests against) is timed beside it
+    at 16 threads."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
@@ -731,15 +736,25 @@ def cpu_dpt_conv(budget_s: float) -> dict:
     x = dpt_values(1, c * h * w)
     wt = dpt_values(2, c * c * 9) * np.float32(1.0 / 34.0)
     b = dpt_values(3, c)
-    times = []
-    start = time.perf_counter()
-    while (not times or time.perf_counter() - start < budget_s) and len(times) < 20:
-        t0 = time.perf_counter()
-        oracle.conv2d_naive(x, c, h, w, wt, c, 3, 3, 1, 1, b)
-        times.append(time.perf_counter() - t0)
-    return {"value": round(float(np.median(times)) * 1e6, 1), "unit": "us",
-            "cores": oracle.threads(), "kind": "port",
-            "sample": f"{len(times)} runs of conv2d_naive 128->128 3x3 at 144x96 (median)"}
+    u = oracle.winograd_f2_filter(wt, c, c)
+    isa = "AVX-512" if oracle.has_avx512() else "scalar"
+    out = {"unit": "us", "kind": "port", "isa": isa}
+    for label, threads in cpu_thread_counts():
+        oracle.set_threads(threads)
+        us, runs = cpu_median_us(lambda: oracle.conv3x3_winograd_f2(x, c, h, w, None, c, b, u=u),
+                                 budget_s=budget_s)
+        out[label] = {"value": round(us, 1), "cores": threads, "runs": runs}
+    oracle.set_threads(16)
+    us, runs = cpu_median_us(lambda: oracle.conv2d_naive(x, c, h, w, wt, c, 3, 3, 1, 1, b),
+                             min_runs=5, budget_s=budget_s, max_runs=20)
+    oracle.set_threads(0)
+    out["conv2d_naive_16_threads"] = {"value": round(us, 1), "cores": 16, "runs": runs}
+    out.update(value=out["16_threads"]["value"], cores=16,
+               sample=(f"Winograd F(2x2,3x3) 128->128 3x3 at 144x96, prepared filter (median of "
+                       f"{out['16_threads']['runs']} warm runs at 16 threads, "
+                       f"{out['affinity_cores']['runs']} at {out['affinity_cores']['cores']} "
+                       f"affinity cores), C restatement of the crate's {isa} path"))
+    return out
 
 
 def cpu_block(budget_s: float, q8_0: bool = False) -> dict:

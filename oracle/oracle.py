@@ -90,6 +90,10 @@ def _declare(L):
     sig("vko_hnd_to_token", None, _f32p, _sz, _sz, _sz, _f32p)
     sig("vko_conv2d_naive", None, _f32p, _sz, _sz, _sz, _f32p, _sz, _sz, _sz, _sz, _sz, _f32p,
         _f32p)
+    sig("vko_winograd_f2_filter", None, _f32p, _sz, _sz, _f32p)
+    sig("vko_conv3x3_winograd_f2", None, _f32p, _sz, _sz, _sz, _f32p, _sz, _f32p, ctypes.c_int,
+        _f32p)
+    sig("vko_winograd_use_lanes", None, ctypes.c_int)
     for name in ("vko_conv_transpose2d", "vko_conv_transpose2d_naive"):
         sig(name, None, _f32p, _sz, _sz, _sz, _f32p, _sz, _sz, _sz, _sz, _f32p, _f32p)
     for name in ("vko_bilinear_resize", "vko_bilinear_resize_naive",
@@ -400,6 +404,34 @@ def conv2d_naive(x, in_c, ih, iw, w, out_c, kh, kw, stride, pad, bias=None):
     b = _opt(bias)
     lib().vko_conv2d_naive(_f(f32(x)), in_c, ih, iw, _f(f32(w)), out_c, kh, kw, stride, pad,
                            _f(b) if b is not None else None, _f(out))
+    return out
+
+
+def winograd_f2_filter(w, in_c, out_c):
+    """conv::transformed_winograd_filter (src/conv.rs:121-173): OIHW 3x3
+    weights -> U [16][in_c][out_c]."""
+    u = np.empty(16 * in_c * out_c, np.float32)
+    lib().vko_winograd_f2_filter(_f(f32(w)), in_c, out_c, _f(u))
+    return u
+
+
+def conv3x3_winograd_f2(x, in_c, ih, iw, w, out_c, bias=None, relu_input=False, u=None,
+                        lanes=False):
+    """The crate's 3x3 stride-1 pad-1 convolution, Winograd F(2x2, 3x3)
+    (src/conv.rs:681-829 with src/specialized.rs:597-633), CHW.  u: a
+    prepared filter (winograd_f2_filter), else w (OIHW) is transformed
+    first.  lanes: the AVX-512 product restated with fmaf."""
+    if u is None:
+        u = winograd_f2_filter(w, in_c, out_c)
+    out = np.empty(out_c * ih * iw, np.float32)
+    b = _opt(bias)
+    lib().vko_winograd_use_lanes(1 if lanes else 0)
+    try:
+        lib().vko_conv3x3_winograd_f2(_f(f32(x)), in_c, ih, iw, _f(u), out_c,
+                                      _f(b) if b is not None else None, 1 if relu_input else 0,
+                                      _f(out))
+    finally:
+        lib().vko_winograd_use_lanes(0)
     return out
 
 

@@ -1331,6 +1331,171 @@ void vko_conv2d_naive(const float *input, size_t in_c, size_t ih, size_t iw, con
             }
 }
 
+/* conv::transformed_winograd_filter (src/conv.rs:121-173): the F(2x2, 3x3)
+ * filter transform U = G g G^T of every (oc, ic) 3x3 kernel with
+ * G = [[1, 0, 0], [1/2, 1/2, 1/2], [1/2, -1/2, 1/2], [0, 0, 1]], rows first
+ * then columns, each sum left to right and then halved, stored
+ * U[position][ic][oc] (output channels innermost). */
+void vko_winograd_f2_filter(const float *weight, size_t in_c, size_t out_c, float *u) {
+    for (size_t oc = 0; oc < out_c; oc++)
+        for (size_t ic = 0; ic < in_c; ic++) {
+            const float *g = weight + (oc * in_c + ic) * 9;
+            float t[4][3], uu[16];
+            for (int j = 0; j < 3; j++) {
+                const float a = g[j], b = g[3 + j], c = g[6 + j];
+                t[0][j] = a;
+                t[1][j] = 0.5f * ((a + b) + c);
+                t[2][j] = 0.5f * ((a - b) + c);
+                t[3][j] = c;
+            }
+            for (int i = 0; i < 4; i++) {
+                const float a = t[i][0], b = t[i][1], c = t[i][2];
+                uu[i * 4] = a;
+                uu[i * 4 + 1] = 0.5f * ((a + b) + c);
+                uu[i * 4 + 2] = 0.5f * ((a - b) + c);
+                uu[i * 4 + 3] = c;
+            }
+            for (int pos = 0; pos < 16; pos++) u[((size_t)pos * in_c + ic) * out_c + oc] = uu[pos];
+        }
+}
+
+/* specialized::winograd_f2_blocked_f32's AVX-512 product
+ * (src/specialized.rs:597-633): per transform position and 16-wide group of
+ * output channels, one accumulator per tile, FMA over the input channels in
+ * order: m[pos][tile][oc] = fma(u[pos][ic][oc], v[pos][ic][tile], .). */
+__attribute__((target("avx512f,fma"))) static void wino_products_avx512(
+    const float *u, const float *v, float *m, size_t in_c, size_t out_c, size_t tiles) {
+    for (size_t pos = 0; pos < 16; pos++) {
+        const float *up = u + pos * in_c * out_c, *vp = v + pos * in_c * tiles;
+        float *mp = m + pos * tiles * out_c;
+        for (size_t o0 = 0; o0 < out_c; o0 += 16) {
+            __m512 acc[8];
+            for (size_t t = 0; t < 8; t++) acc[t] = _mm512_setzero_ps();
+            for (size_t ic = 0; ic < in_c; ic++) {
+                const __m512 f = _mm512_loadu_ps(up + ic * out_c + o0);
+                for (size_t t = 0; t < tiles; t++)
+                    acc[t] = _mm512_fmadd_ps(f, _mm512_set1_ps(vp[ic * tiles + t]), acc[t]);
+            }
+            for (size_t t = 0; t < tiles; t++) _mm512_storeu_ps(mp + t * out_c + o0, acc[t]);
+        }
+    }
+}
+
+/* The same product lane by lane (fmaf in the same order), for the bitwise
+ * check of the AVX-512 form. */
+static void wino_products_lanes(const float *u, const float *v, float *m, size_t in_c,
+                                size_t out_c, size_t tiles) {
+    for (size_t pos = 0; pos < 16; pos++)
+        for (size_t t = 0; t < tiles; t++)
+            for (size_t oc = 0; oc < out_c; oc++) {
+                float acc = 0.0f;
+                for (size_t ic = 0; ic < in_c; ic++)
+                    acc = fmaf(u[(pos * in_c + ic) * out_c + oc], v[(pos * in_c + ic) * tiles + t], acc);
+                m[(pos * tiles + t) * out_c + oc] = acc;
+            }
+}
+
+/* The crate's scalar fallback product (src/conv.rs:775-788): unfused
+ * sum += u * v from 0 over the input channels. */
+static void wino_products_scalar(const float *u, const float *v, float *m, size_t in_c,
+                                 size_t out_c, size_t tiles) {
+    for (size_t pos = 0; pos < 16; pos++)
+        for (size_t t = 0; t < tiles; t++)
+            for (size_t oc = 0; oc < out_c; oc++) {
+                float sum = 0.0f;
+                for (size_t ic = 0; ic < in_c; ic++)
+                    sum = sum + u[(pos * in_c + ic) * out_c + oc] * v[(pos * in_c + ic) * tiles + t];
+                m[(pos * tiles + t) * out_c + oc] = sum;
+            }
+}
+
+/* 0: the crate's dispatch (AVX-512 product when avx512f+fma and out_c % 16
+ * == 0, else its scalar product); 1: the AVX-512 product restated with fmaf. */
+static int g_wino_lanes = 0;
+void vko_winograd_use_lanes(int on) { g_wino_lanes = on ? 1 : 0; }
+
+/* conv::conv3x3_winograd_f2_impl (src/conv.rs:681-829): 3x3, stride 1,
+ * pad 1, CHW.  Output tiles of 2x2 in row-major order, in blocks of four
+ * (winograd_tile_block, src/conv.rs:30-39) run in parallel (at least four
+ * blocks per task, src/conv.rs:41-51, here OpenMP chunks of four blocks).
+ * Per block:
+ *  - input transform B^T d B of each tile's 4x4 patch (zero outside the
+ *    image; max(x, 0) first when relu_input), columns then rows, stored
+ *    v[position][ic][tile];
+ *  - the per-position product over the input channels (above);
+ *  - output transform A^T m A, left to right, plus the bias, written to the
+ *    tile's 2x2 outputs inside the image. */
+void vko_conv3x3_winograd_f2(const float *input, size_t in_c, size_t ih, size_t iw,
+                             const float *u, size_t out_c, const float *bias, int relu_input,
+                             float *out) {
+    const size_t oh = ih, ow = iw, tiles_x = (ow + 1) / 2, tiles_y = (oh + 1) / 2;
+    const size_t tiles = tiles_x * tiles_y, tb = 4, blocks = (tiles + tb - 1) / tb;
+    const int avx = !g_wino_lanes && has_avx512f_fma() && out_c % 16 == 0;
+#pragma omp parallel OMP_THREADS
+    {
+        float *v = malloc(16 * in_c * tb * sizeof(float));
+        float *prod = malloc(16 * tb * out_c * sizeof(float));
+#pragma omp for schedule(dynamic, 4)
+        for (size_t blk = 0; blk < blocks; blk++) {
+            const size_t tile0 = blk * tb, active = tiles - tile0 < tb ? tiles - tile0 : tb;
+            for (size_t lt = 0; lt < active; lt++) {
+                const size_t tile = tile0 + lt, y = tile / tiles_x * 2, x = tile % tiles_x * 2;
+                for (size_t ic = 0; ic < in_c; ic++) {
+                    float d[16], col[16];
+                    for (int dy = 0; dy < 4; dy++)
+                        for (int dx = 0; dx < 4; dx++) {
+                            const long sy = (long)y + dy - 1, sx = (long)x + dx - 1;
+                            float smp = 0.0f;
+                            if (sy >= 0 && sy < (long)ih && sx >= 0 && sx < (long)iw)
+                                smp = input[(ic * ih + (size_t)sy) * iw + (size_t)sx];
+                            d[dy * 4 + dx] = relu_input ? rmax(smp, 0.0f) : smp;
+                        }
+                    for (int j = 0; j < 4; j++) {
+                        const float a = d[j], b = d[4 + j], c = d[8 + j], e = d[12 + j];
+                        col[j] = a - c;
+                        col[4 + j] = b + c;
+                        col[8 + j] = c - b;
+                        col[12 + j] = b - e;
+                    }
+                    for (int i = 0; i < 4; i++) {
+                        const float a = col[i * 4], b = col[i * 4 + 1], c = col[i * 4 + 2],
+                                    e = col[i * 4 + 3];
+                        v[((size_t)(i * 4) * in_c + ic) * active + lt] = a - c;
+                        v[((size_t)(i * 4 + 1) * in_c + ic) * active + lt] = b + c;
+                        v[((size_t)(i * 4 + 2) * in_c + ic) * active + lt] = c - b;
+                        v[((size_t)(i * 4 + 3) * in_c + ic) * active + lt] = b - e;
+                    }
+                }
+            }
+            if (avx) wino_products_avx512(u, v, prod, in_c, out_c, active);
+            else if (g_wino_lanes) wino_products_lanes(u, v, prod, in_c, out_c, active);
+            else wino_products_scalar(u, v, prod, in_c, out_c, active);
+            for (size_t lt = 0; lt < active; lt++) {
+                const size_t tile = tile0 + lt, ty = tile / tiles_x, tx = tile % tiles_x;
+                for (size_t oc = 0; oc < out_c; oc++) {
+                    float p[8];
+#define WM(pos) prod[((size_t)(pos) * active + lt) * out_c + oc]
+                    for (int j = 0; j < 4; j++) {
+                        p[j] = (WM(j) + WM(4 + j)) + WM(8 + j);
+                        p[4 + j] = (WM(4 + j) - WM(8 + j)) - WM(12 + j);
+                    }
+#undef WM
+                    const float b = bias ? bias[oc] : 0.0f;
+                    const float vals[4] = {((p[0] + p[1]) + p[2]) + b, ((p[1] - p[2]) - p[3]) + b,
+                                           ((p[4] + p[5]) + p[6]) + b, ((p[5] - p[6]) - p[7]) + b};
+                    for (int dy = 0; dy < 2; dy++)
+                        for (int dx = 0; dx < 2; dx++) {
+                            const size_t oy = ty * 2 + dy, ox = tx * 2 + dx;
+                            if (oy < oh && ox < ow) out[(oc * oh + oy) * ow + ox] = vals[dy * 2 + dx];
+                        }
+                }
+            }
+        }
+        free(v);
+        free(prod);
+    }
+}
+
 /* conv::conv_transpose2d (src/conv.rs:1009-1098), its three routes:
  *  - kernel == stride and in_c % 16 == 0 on an AVX-512 host: the prepacked
  *    non-overlap kernel (src/specialized.rs:206-271): sixteen FMA lanes over

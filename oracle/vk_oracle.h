@@ -160,6 +160,17 @@ void vko_vit_block_q8_0(float *x, size_t images, size_t tokens, const vko_block_
 void vko_conv2d_naive(const float *input, size_t in_c, size_t ih, size_t iw, const float *weight,
                       size_t out_c, size_t kh, size_t kw, size_t stride, size_t pad,
                       const float *bias, float *out);
+/* Winograd F(2x2, 3x3), the crate's CPU route for 3x3 stride-1 pad-1
+ * convolutions (conv::conv2d, src/conv.rs:897-900): the filter transform
+ * (src/conv.rs:121-173) into u [16][in_c][out_c], then the tiled convolution
+ * (src/conv.rs:681-829) with the AVX-512 product of src/specialized.rs:597-633
+ * (or the crate's scalar product).  out [out_c][ih][iw]. */
+void vko_winograd_f2_filter(const float *weight, size_t in_c, size_t out_c, float *u);
+void vko_conv3x3_winograd_f2(const float *input, size_t in_c, size_t ih, size_t iw,
+                             const float *u, size_t out_c, const float *bias, int relu_input,
+                             float *out);
+/* 1: the AVX-512 product restated lane by lane with fmaf (bitwise check). */
+void vko_winograd_use_lanes(int on);
 /* conv_transpose2d (src/conv.rs:1009-1098) with its three routes; weight
  * IOHW, oh = (ih-1)*stride + kh. */
 void vko_conv_transpose2d(const float *input, size_t in_c, size_t ih, size_t iw,

@@ -5,9 +5,10 @@ Convolutions run as fp32-MFMA GEMMs, so they are held to the f32
 accumulation bound against the crate's direct oracle: |gpu - naive| <=
 (K + 2) * 6e-8 * sum|x||w| per output (K taps).  The gather-form transposed
 convolution and the resizes restate the reference's op order and are
-bit-exact; the fused variants (ReLU input, resize + add + conv) are checked
-bit for bit against their materialised routes, as the crate's own tests do
-(src/conv.rs:1479-1600)."""
+bit-exact.  3x3 stride-1 convolutions are also compared with the crate's own
+CPU route for them, Winograd F(2x2, 3x3).  The fused variants (ReLU input,
+resize + add + conv) are checked bit for bit against their materialised
+routes, as the crate's own tests do (src/conv.rs:1479-1600)."""
 import numpy as np
 import pytest
 
@@ -60,6 +61,23 @@ def test_conv2d_vs_naive(rt, in_c, out_c, ih, iw, k, s, p):
     got = rt.download_f32(conv.run(rt.upload_f32(x), ih, iw))
     exp = O.conv2d_naive(x, in_c, ih, iw, w, out_c, k, k, s, p, b)
     assert np.all(np.abs(got.astype(np.float64) - exp) <= _conv_bound(x, in_c, ih, iw, w, out_c, k, s, p, b))
+
+
+@pytest.mark.parametrize("in_c, out_c, ih, iw", [(96, 128, 24, 36), (64, 32, 48, 72),
+                                                 (128, 128, 96, 144), (16, 16, 7, 9)])
+def test_conv3x3_vs_crate_winograd(rt, in_c, out_c, ih, iw):
+    """The crate computes 3x3 stride-1 pad-1 convolutions with Winograd F(2x2,
+    3x3) (conv::conv2d, src/conv.rs:897-900), not with the direct sum.  The
+    device's direct convolution and that route each hold the f32 accumulation
+    bound of the exact convolution (the oracle's Winograd is pinned to it on
+    the CPU), so they agree within twice the bound."""
+    x, w, b = _data(0xF2F2A000 + in_c + ih, in_c * ih * iw, out_c * in_c * 9, out_c)
+    w = w * np.float32(1.0 / np.sqrt(in_c * 9))
+    conv = rt.prepare_conv2d_f32(in_c, out_c, 3, 3, 1, 1, w, b)
+    got = rt.download_f32(conv.run(rt.upload_f32(x), ih, iw))
+    wino = O.conv3x3_winograd_f2(x, in_c, ih, iw, w, out_c, b)
+    bound = 2 * _conv_bound(x, in_c, ih, iw, w, out_c, 3, 1, 1, b)
+    assert np.all(np.abs(got.astype(np.float64) - wino) <= bound)
 
 
 def test_conv2d_hand_checked_and_one_shot(rt):

@@ -166,6 +166,97 @@ def test_conv2d_naive_is_the_definition(in_c, out_c, ih, iw, k, s, p):
         assert np.abs(O.conv2d_naive(x, in_c, ih, iw, wt, out_c, k, k, s, p, b) - got).max() > 1e-3
 
 
+# ---- Winograd F(2x2, 3x3): the crate's CPU route for 3x3 stride-1 pad-1 -----------
+
+def test_winograd_f2_matches_direct_oracle_reference_case():
+    """src/conv.rs:1438-1477: in_c 3, out_c 5, 7 x 9, Xorshift32(0xF2F2_0001)
+    drawing input, weight and bias in that order; |winograd - naive| < 2e-5."""
+    in_c, out_c, h, w = 3, 5, 7, 9
+    r = O.xorshift32_vec(0xF2F20001, in_c * h * w + out_c * in_c * 9 + out_c)
+    x, wt, b = r[:in_c * h * w], r[in_c * h * w:-out_c], r[-out_c:]
+    got = O.conv3x3_winograd_f2(x, in_c, h, w, wt, out_c, b)
+    direct = O.conv2d_naive(x, in_c, h, w, wt, out_c, 3, 3, 1, 1, b)
+    assert np.abs(got - direct).max() < 2e-5
+
+
+@pytest.mark.parametrize("in_c, out_c, ih, iw", [(3, 5, 7, 9), (16, 32, 13, 11), (64, 32, 5, 4),
+                                                 (96, 128, 24, 36), (1, 16, 1, 1)])
+def test_winograd_f2_is_the_convolution(in_c, out_c, ih, iw):
+    """Against the float64 definition within the f32 accumulation bound, at odd
+    sizes (edge tiles half outside the image) and DPT shapes; the transposed
+    kernel (kx <-> ky) must miss, so a swapped transform index cannot pass."""
+    n = in_c * ih * iw + out_c * in_c * 9 + out_c
+    r = O.xorshift32_vec(0xF2F2 + in_c + ih, n)
+    x, w, b = r[:in_c * ih * iw], r[in_c * ih * iw:n - out_c], r[n - out_c:]
+    w = w * np.float32(1.0 / np.sqrt(in_c * 9))
+    got = O.conv3x3_winograd_f2(x, in_c, ih, iw, w, out_c, b)
+    exact = conv_f64(x, in_c, ih, iw, w, out_c, 3, 1, 1, b)
+    absb = conv_f64(np.abs(x), in_c, ih, iw, np.abs(w), out_c, 3, 1, 1, np.abs(b))
+    assert np.all(np.abs(got - exact) <= f32_bound(in_c * 9 + 16, absb))
+    wt = np.ascontiguousarray(w.reshape(out_c, in_c, 3, 3).transpose(0, 1, 3, 2)).reshape(-1)
+    if ih > 1 and iw > 1:
+        assert np.abs(O.conv3x3_winograd_f2(x, in_c, ih, iw, wt, out_c, b) - got).max() > 1e-3
+
+
+def test_winograd_f2_filter_is_g_g_gt():
+    """U = G g G^T per (oc, ic), stored [position][ic][oc]."""
+    in_c, out_c = 3, 2
+    w = O.xorshift32_vec(0xF117, out_c * in_c * 9)
+    u = O.winograd_f2_filter(w, in_c, out_c).reshape(16, in_c, out_c)
+    G = np.array([[1, 0, 0], [0.5, 0.5, 0.5], [0.5, -0.5, 0.5], [0, 0, 1]])
+    g = np.asarray(w, np.float64).reshape(out_c, in_c, 3, 3)
+    for oc in range(out_c):
+        for ic in range(in_c):
+            exp = (G @ g[oc, ic] @ G.T).reshape(16)
+            assert np.abs(u[:, ic, oc] - exp).max() <= 4e-7 * (np.abs(g[oc, ic]).sum() + 1e-30)
+
+
+@pytest.mark.skipif(not O.has_avx512(), reason="host without AVX-512")
+def test_winograd_f2_avx512_product_is_its_lane_restatement():
+    """The AVX-512 product (one FMA chain per lane over the input channels)
+    equals its fmaf restatement bit for bit, edge tiles and a partial last
+    tile block included."""
+    in_c, out_c, ih, iw = 48, 32, 9, 13
+    x = O.xorshift32_vec(0xA5, in_c * ih * iw)
+    w = O.xorshift32_vec(0xA6, out_c * in_c * 9)
+    b = O.xorshift32_vec(0xA7, out_c)
+    u = O.winograd_f2_filter(w, in_c, out_c)
+    a = O.conv3x3_winograd_f2(x, in_c, ih, iw, None, out_c, b, u=u)
+    lanes = O.conv3x3_winograd_f2(x, in_c, ih, iw, None, out_c, b, u=u, lanes=True)
+    assert np.array_equal(a.view(np.uint32), lanes.view(np.uint32))
+
+
+def test_winograd_f2_scalar_tier_is_the_convolution():
+    """The crate's scalar product (unfused sums, src/conv.rs:775-788), taken
+    on hosts without AVX-512 and for out_c % 16 != 0."""
+    in_c, out_c, ih, iw = 8, 16, 6, 7
+    n = in_c * ih * iw + out_c * in_c * 9 + out_c
+    r = O.xorshift32_vec(0x5CA1, n)
+    x, w, b = r[:in_c * ih * iw], r[in_c * ih * iw:n - out_c], r[n - out_c:]
+    O.force_scalar(True)
+    try:
+        got = O.conv3x3_winograd_f2(x, in_c, ih, iw, w, out_c, b)
+    finally:
+        O.force_scalar(False)
+    exact = conv_f64(x, in_c, ih, iw, w, out_c, 3, 1, 1, b)
+    absb = conv_f64(np.abs(x), in_c, ih, iw, np.abs(w), out_c, 3, 1, 1, np.abs(b))
+    assert np.all(np.abs(got - exact) <= f32_bound(in_c * 9 + 16, absb))
+
+
+def test_winograd_relu_input_equals_materialised_relu_bitwise():
+    """src/conv.rs:1479-1519: ReLU applied while loading the patches gives the
+    bits of the convolution of the materialised ReLU."""
+    in_c, out_c, h, w = 3, 5, 7, 9
+    i = np.arange(in_c * h * w, dtype=np.float32)
+    x = ((np.sin(i * np.float32(0.17)) - np.float32(0.4)) * np.float32(1.3)).astype(np.float32)
+    wt = (np.cos(np.arange(out_c * in_c * 9, dtype=np.float32) * np.float32(0.11))
+          * np.float32(0.2)).astype(np.float32)
+    b = (np.arange(out_c, dtype=np.float32) * np.float32(0.03) - np.float32(0.05)).astype(np.float32)
+    expected = O.conv3x3_winograd_f2(np.maximum(x, 0), in_c, h, w, wt, out_c, b)
+    actual = O.conv3x3_winograd_f2(x, in_c, h, w, wt, out_c, b, relu_input=True)
+    assert np.array_equal(actual.view(np.uint32), expected.view(np.uint32))
+
+
 def bilinear_f64(x, c, ih, iw, oh, ow, align):
     """The sampling definitions in float64: half-pixel src = (d+0.5)*in/out - 0.5
     clamped to the edge; align-corners src = d*(in-1)/(out-1)."""
