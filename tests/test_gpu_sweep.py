@@ -1,0 +1,101 @@
+"""Randomized-shape parity sweep of the device projections, attention and
+Q8_0 GEMM (fixed seed, so every run draws the same cases).
+
+The per-shape tests elsewhere pin the DA3 shapes and the tiling edges that
+the kernels' own logic names; this sweep adds ragged sizes nobody picked by
+hand (M, K, N from 1 to a few thousand, round, near-round and arbitrary),
+so that a tile, split or tail choice taken only for some shape class is
+exercised with its neighbours.  Bars:
+- projections (linear_bias_scale_f32_da3_base's Store, the fused GELU and
+  Residual epilogues, src/specialized.rs:811-929) against float64, within
+  the f32 accumulation bound (K + 2) * 6e-8 * (|A||W| + |b|) per output, the
+  epilogue's own roundings, and for GELU the fast form's 1e-6 * max(1, |v|)
+  (the erf of the float64 reference is exact to double precision);
+- DA3 flash attention against float64 softmax attention, 2e-5 * max |V|;
+- the Q8_0 GEMM (Kernels::gemm_q8_0, src/dispatch.rs:91-105) bit for bit
+  against the oracle.
+"""
+import numpy as np
+import pytest
+from scipy.special import erf
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+_RNG = np.random.default_rng(20261202)
+
+
+def _dim(lo, hi):
+    r = _RNG.random()
+    if r < 0.3:
+        return int(_RNG.integers(lo, hi + 1))
+    if r < 0.6:
+        return int(min(hi, max(lo, 32 * _RNG.integers(1, hi // 32 + 1))))
+    return int(min(hi, max(lo, 16 * _RNG.integers(1, hi // 16 + 1) + _RNG.integers(-2, 3))))
+
+
+PROJ_CASES = [(str(_RNG.choice(["store", "gelu", "residual"])), _dim(1, 2000), _dim(1, 1600),
+               _dim(1, 2500), bool(_RNG.random() < 0.6), int(_RNG.integers(1, 1 << 30)))
+              for _ in range(36)]
+FLASH_CASES = [(int(_RNG.integers(1, 7)), _dim(1, 1800), bool(_RNG.random() < 0.5),
+                int(_RNG.integers(1, 1 << 30))) for _ in range(14)]
+Q8_CASES = [(_dim(1, 2000), _dim(1, 2100), 32 * int(_RNG.integers(1, 80)),
+             int(_RNG.integers(1, 1 << 30))) for _ in range(12)]
+
+
+@pytest.mark.parametrize("mode, m, k, n, gamma, seed", PROJ_CASES)
+def test_projection_random_shapes_vs_float64(rt, mode, m, k, n, gamma, seed):
+    rng = np.random.default_rng(seed)
+    a = rng.standard_normal(m * k).astype(np.float32)
+    w = (rng.standard_normal(k * n) * 0.05).astype(np.float32)
+    b = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    g = (0.1 + rng.random(n)).astype(np.float32) if gamma and mode != "gelu" else None
+    lin = rt.prepare_linear_f32(k, n, w, b, g)
+    A, W = a.reshape(m, k).astype(np.float64), w.reshape(k, n).astype(np.float64)
+    v = A @ W + b
+    bv = (k + 2) * 6e-8 * (np.abs(A) @ np.abs(W) + np.abs(b)) + 1e-30
+    gg = np.ones(n) if g is None else g.astype(np.float64)
+    if mode == "store":
+        got = rt.download_f32(lin.run(rt.upload_f32(a), m)).reshape(m, n)
+        exp = v * gg
+        bound = bv * gg + 6e-8 * np.abs(exp)
+    elif mode == "gelu":
+        got = rt.download_f32(lin.run_gelu(rt.upload_f32(a), m)).reshape(m, n)
+        exp = 0.5 * v * (1 + erf(v / np.sqrt(2)))
+        bound = 1.2 * bv + 2e-6 * np.maximum(1, np.abs(v))
+    else:
+        x = rng.standard_normal(m * n).astype(np.float32)
+        xt = rt.upload_f32(x)
+        lin.run_residual(rt.upload_f32(a), m, xt)
+        got = rt.download_f32(xt).reshape(m, n)
+        exp = x.reshape(m, n) + v * gg
+        bound = bv * gg + 1.2e-7 * (np.abs(exp) + np.abs(x.reshape(m, n)))
+    assert np.all(np.abs(got - exp) <= bound), float((np.abs(got - exp) / bound).max())
+
+
+@pytest.mark.parametrize("heads, tokens, token_major, seed", FLASH_CASES)
+def test_flash_random_shapes_vs_float64(rt, heads, tokens, token_major, seed):
+    rng = np.random.default_rng(seed)
+    q, k, v = (rng.standard_normal(heads * tokens * 64).astype(np.float32) for _ in range(3))
+    got = rt.download_f32(rt.flash_attention_f32_da3_base(
+        rt.upload_f32(q), rt.upload_f32(k), rt.upload_f32(v), heads, tokens, token_major))
+    Q, K, V = (t.reshape(heads, tokens, 64).astype(np.float64) for t in (q, k, v))
+    s = Q @ K.transpose(0, 2, 1) / 8.0
+    p = np.exp(s - s.max(-1, keepdims=True))
+    o = (p / p.sum(-1, keepdims=True)) @ V
+    if token_major:
+        o = o.transpose(1, 0, 2)
+    assert np.abs(got - o.reshape(-1)).max() <= 2e-5 * np.abs(V).max()
+
+
+@pytest.mark.parametrize("m, n, k, seed", Q8_CASES)
+def test_gemm_q8_0_random_shapes_bit_exact(rt, m, n, k, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w = (rng.standard_normal(n * k) * 0.02).astype(np.float32)
+    exp = O.gemm_q8_0(O.quantize_rows_q8_0(x, m, k), O.quantize_rows_q8_0(w, n, k), m, n, k,
+                      impl="kernels")
+    got = rt.download_f32(rt.gemm_q8_0(rt.quantize_q8_0(rt.upload_f32(x), m, k),
+                                       rt.quantize_q8_0(rt.upload_f32(w), n, k), m, n, k))
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
