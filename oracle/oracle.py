@@ -90,6 +90,9 @@ def _declare(L):
     sig("vko_hnd_to_token", None, _f32p, _sz, _sz, _sz, _f32p)
     sig("vko_conv2d_naive", None, _f32p, _sz, _sz, _sz, _f32p, _sz, _sz, _sz, _sz, _sz, _f32p,
         _f32p)
+    sig("vko_expf_glibc_form", ctypes.c_float, ctypes.c_float)
+    sig("vko_exp2f_table_entry", ctypes.c_uint64, ctypes.c_int)
+    sig("vko_expf_form_mismatches", ctypes.c_uint64, ctypes.c_uint32)
     sig("vko_winograd_f2_filter", None, _f32p, _sz, _sz, _f32p)
     sig("vko_conv3x3_winograd_f2", None, _f32p, _sz, _sz, _sz, _f32p, _sz, _f32p, ctypes.c_int,
         _f32p)
@@ -405,6 +408,20 @@ def conv2d_naive(x, in_c, ih, iw, w, out_c, kh, kw, stride, pad, bias=None):
     lib().vko_conv2d_naive(_f(f32(x)), in_c, ih, iw, _f(f32(w)), out_c, kh, kw, stride, pad,
                            _f(b) if b is not None else None, _f(out))
     return out
+
+
+def expf_glibc_form(x: float) -> float:
+    """glibc 2.35's expf algorithm restated (the device GELU tail's expf)."""
+    return float(lib().vko_expf_glibc_form(ctypes.c_float(x)))
+
+
+def exp2f_table_entry(i: int) -> int:
+    return int(lib().vko_exp2f_table_entry(i))
+
+
+def expf_form_mismatches(step: int = 1) -> int:
+    """Bit patterns (every step-th) where the restatement differs from the host's expf."""
+    return int(lib().vko_expf_form_mismatches(step))
 
 
 def winograd_f2_filter(w, in_c, out_c):

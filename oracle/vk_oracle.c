@@ -224,6 +224,76 @@ void vko_layernorm(float *x, size_t rows, size_t cols, const float *gamma, const
     for (size_t r = 0; r < rows; r++) layernorm_row(x + r * cols, cols, gamma, beta, eps);
 }
 
+/* The expf that f32::exp calls on Linux (src/scalar.rs:132 uses it): glibc
+ * 2.35 on x86-64 with FMA, whose published design is ARM
+ * optimized-routines' expf (in glibc since 2.27).  x * 32/ln2 = k + r, k
+ * rounded to an integer by adding 1.5 * 2^52; 2^(k/32) from a table of the
+ * correctly rounded 2^(i/32) with i << 47 taken off each entry's bits, so
+ * that adding k << 47 carries k / 32 into the exponent; 2^(r/32) by a cubic;
+ * double precision with every multiply-add fused, one rounding to float.
+ * The oracle itself calls the host's expf; this restatement exists to pin
+ * the device's transcription (gelu_scalar_form's glibc_expf) against it:
+ * vko_expf_form_mismatches counts where the two differ. */
+static const uint64_t EXP2F_TAB[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+uint64_t vko_exp2f_table_entry(int i) { return EXP2F_TAB[i & 31]; }
+
+float vko_expf_glibc_form(float x) {
+    uint32_t bits;
+    memcpy(&bits, &x, 4);
+    const uint32_t abstop = (bits >> 20) & 0x7ff;
+    if (abstop >= 0x42b) {             /* |x| >= 88, inf or NaN */
+        if (bits == 0xff800000u) return 0.0f;
+        if (abstop >= 0x7f8) return x + x;
+        if (x > 0x1.62e42ep6f) return INFINITY;
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    double kd = fma(inv_ln2_n, xd, shift);
+    uint64_t ki, sb;
+    memcpy(&ki, &kd, 8);
+    kd -= shift;
+    const double r = fma(inv_ln2_n, xd, -kd);
+    sb = EXP2F_TAB[ki % 32] + (ki << 47);
+    double s;
+    memcpy(&s, &sb, 8);
+    const double z = fma(c0, r, c1), r2 = r * r;
+    const double y = fma(z, r2, fma(c2, r, 1.0));
+    return (float)(y * s);
+}
+
+/* Inputs u = 0, step, 2 step, ... (all 2^32 bit patterns at step 1) where the
+ * restatement differs from the host's expf (NaN results compared as NaN). */
+uint64_t vko_expf_form_mismatches(uint32_t step) {
+    uint64_t bad = 0;
+    if (step == 0) step = 1;
+#pragma omp parallel for OMP_THREADS reduction(+ : bad) schedule(static)
+    for (long long u = 0; u < (1LL << 32); u += step) {
+        const uint32_t b = (uint32_t)u;
+        float x, e, c;
+        memcpy(&x, &b, 4);
+        e = expf(x);
+        c = vko_expf_glibc_form(x);
+        if (isnan(e) && isnan(c)) continue;
+        uint32_t be, bc;
+        memcpy(&be, &e, 4);
+        memcpy(&bc, &c, 4);
+        bad += be != bc;
+    }
+    return bad;
+}
+
 /* src/scalar.rs:126-134 -- Abramowitz-Stegun 7.1.26, every op separately rounded. */
 float vko_erf(float x) {
     float s = isnan(x) ? x : copysignf(1.0f, x); /* f32::signum */

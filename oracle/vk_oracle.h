@@ -154,6 +154,14 @@ void vko_vit_block_q8_0(float *x, size_t images, size_t tokens, const vko_block_
                         const int64_t *pos_yx, float rope_freq, float eps, float *tap_ln1,
                         float *tap_attn, float *tap_gelu);
 
+/* glibc 2.35's expf algorithm restated (the device's gelu_scalar_form uses
+ * the same arithmetic): the value, one entry of its 2^(i/32) table, and the
+ * number of sampled inputs (every step-th bit pattern) where it differs from
+ * the host's expf. */
+float vko_expf_glibc_form(float x);
+uint64_t vko_exp2f_table_entry(int i);
+uint64_t vko_expf_form_mismatches(uint32_t step);
+
 /* ---- DPT head (src/conv.rs, src/resample.rs); batch-1 CHW ------------- */
 /* conv2d_naive (src/conv.rs:950-998): weight OIHW, bias [out_c] or NULL,
  * oh = (ih + 2*pad - kh)/stride + 1. */

@@ -492,7 +492,8 @@ def test_layernorm_da3_shape(rt):
 @pytest.mark.parametrize("n", [1000, 2657280, 17])
 def test_gelu_vs_kernels_gelu(rt, n):
     """tests/simd_matches_scalar.rs ramp plus the fc1 size; AVX-512 form on
-    the n - n%16 prefix, scalar form on the tail."""
+    the n - n%16 prefix, scalar form (with the host libm's expf) on the
+    tail, both bit for bit."""
     x = (np.arange(n, dtype=np.float32) * np.float32(0.017) - np.float32(3.0)) if n == 1000 \
         else seeded.normal(60 + n, n, 2.0)
     exp = O.gelu_avx512_lanes(x)
@@ -501,7 +502,25 @@ def test_gelu_vs_kernels_gelu(rt, n):
     got = rt.download_f32(t)
     main = n - n % 16
     assert_bits_equal(got[:main], exp[:main], "AVX-512-form GELU")
-    assert np.abs(got[main:] - exp[main:]).max(initial=0.0) <= 2e-6
+    assert_bits_equal(got[main:], exp[main:], "scalar-form GELU tail")
+
+
+def test_gelu_scalar_tail_bit_exact(rt):
+    """Arrays shorter than 16 run wholly in Kernels::gelu's scalar tail
+    (scalar::gelu, src/scalar.rs:116-134, whose exp is the host libm's expf,
+    which the device restates): 4000 arrays of 15 values, uniform over
+    [-15, 15] (exp's argument down past its underflow) and N(0, 2^2), bit for
+    bit against the oracle."""
+    rng = np.random.default_rng(0x6E1)
+    vals = np.concatenate([rng.uniform(-15, 15, 30000),
+                           rng.standard_normal(30000) * 2]).astype(np.float32)
+    got = np.empty_like(vals)
+    for i in range(0, vals.size, 15):
+        t = rt.upload_f32(vals[i:i + 15])
+        rt.gelu_f32_in_place(t)
+        got[i:i + 15] = rt.download_f32(t)
+    exp = np.concatenate([O.kernels_gelu(vals[i:i + 15]) for i in range(0, vals.size, 15)])
+    assert_bits_equal(got, exp, "scalar GELU")
 
 
 def test_rope2d_bit_exact_with_host_table(rt):

@@ -13,13 +13,17 @@ exercised with its neighbours.  Bars:
   (the erf of the float64 reference is exact to double precision);
 - DA3 flash attention against float64 softmax attention, 2e-5 * max |V|;
 - the Q8_0 GEMM (Kernels::gemm_q8_0, src/dispatch.rs:91-105) bit for bit
-  against the oracle.
+  against the oracle, and the Q8_0 projections (bias, LayerScale, GELU,
+  residual) bit for bit against the oracle's composition of the engine's
+  passes.
 """
 import numpy as np
 import pytest
 from scipy.special import erf
 
 import oracle as O
+from conftest import assert_bits_equal
+from q8_compose import q8_linear, weight_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -40,6 +44,9 @@ PROJ_CASES = [(str(_RNG.choice(["store", "gelu", "residual"])), _dim(1, 2000), _
               for _ in range(36)]
 FLASH_CASES = [(int(_RNG.integers(1, 7)), _dim(1, 1800), bool(_RNG.random() < 0.5),
                 int(_RNG.integers(1, 1 << 30))) for _ in range(14)]
+Q8_LINEAR_CASES = [(str(_RNG.choice(["store", "gelu", "residual"])), _dim(1, 1500),
+                    32 * int(_RNG.integers(1, 60)), _dim(1, 2000), bool(_RNG.random() < 0.5),
+                    int(_RNG.integers(1, 1 << 30))) for _ in range(10)]
 Q8_CASES = [(_dim(1, 2000), _dim(1, 2100), 32 * int(_RNG.integers(1, 80)),
              int(_RNG.integers(1, 1 << 30))) for _ in range(12)]
 
@@ -99,3 +106,24 @@ def test_gemm_q8_0_random_shapes_bit_exact(rt, m, n, k, seed):
     got = rt.download_f32(rt.gemm_q8_0(rt.quantize_q8_0(rt.upload_f32(x), m, k),
                                        rt.quantize_q8_0(rt.upload_f32(w), n, k), m, n, k))
     assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+@pytest.mark.parametrize("mode, m, k, n, gamma, seed", Q8_LINEAR_CASES)
+def test_q8_linear_random_shapes_bit_exact(rt, mode, m, k, n, gamma, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    g = (0.1 + rng.random(n)).astype(np.float32) if gamma and mode != "gelu" else None
+    wb = weight_blocks(w, k, n)
+    lin = rt.prepare_linear_q8_0(k, n, wb, bias, g)
+    xt = rt.upload_f32(x)
+    if mode == "residual":
+        r = rng.standard_normal(m * n).astype(np.float32)
+        rt_r = rt.upload_f32(r)
+        lin.run_residual(xt, m, rt_r)
+        got, exp = rt.download_f32(rt_r), q8_linear(x, m, k, n, wb, bias, g, "residual", r)
+    else:
+        got = rt.download_f32(lin.run_gelu(xt, m) if mode == "gelu" else lin.run(xt, m))
+        exp = q8_linear(x, m, k, n, wb, bias, g, mode)
+    assert_bits_equal(got, exp, f"Q8_0 linear {mode} {m}x{k}x{n}")

@@ -146,3 +146,40 @@ def test_gelu_lane_restatement_is_bitwise_avx512():
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     tail = x[-(x.size % 16):]
     assert np.array_equal(a[-tail.size:], O.gelu(tail))  # n % 16 tail is scalar::gelu
+
+
+# ---- the host libm's expf, restated for the device's scalar GELU tail -----------
+
+def test_exp2f_table_is_the_correctly_rounded_powers_of_two():
+    """Entry i is the bits of 2^(i/32) rounded to double, minus i << 47: 2^(i/32)
+    from 60-digit decimal arithmetic, rounded by float()."""
+    from decimal import Decimal, getcontext
+    import struct
+    getcontext().prec = 60
+    ln2 = Decimal(2).ln()
+    for i in range(32):
+        d = float((Decimal(i) / 32 * ln2).exp())
+        bits = struct.unpack("<Q", struct.pack("<d", d))[0]
+        assert O.exp2f_table_entry(i) == bits - (i << 47), i
+
+
+def test_expf_restatement_equals_host_expf_for_every_input():
+    """All 2^32 bit patterns (NaN results compared as NaN): the restated
+    algorithm is the host's expf (glibc, which f32::exp calls on Linux), so
+    the device's transcription of it gives the crate's bits in the GELU tail."""
+    assert O.expf_form_mismatches(1) == 0
+
+
+def test_device_gelu_tail_uses_the_restated_expf():
+    """The device's glibc_expf (common.h) carries the oracle's table and
+    constants digit for digit."""
+    import re
+    from pathlib import Path
+    src = (Path(__file__).resolve().parents[1] / "vestra-kernels_amd/csrc/common.h").read_text()
+    body = src[src.index("float glibc_expf(float x)"):src.index("float gelu_scalar_form(float v)")]
+    tab = [int(t, 16) for t in re.findall(r"0x([0-9a-f]{16})ull", body)]
+    assert tab == [O.exp2f_table_entry(i) for i in range(32)]
+    for c in ("0x1.71547652b82fep+0", "0x1.8p+52", "0x1.c6af84b912394p-5", "0x1.ebfce50fac4f3p-3",
+              "0x1.62e42ff0c52d6p-1", "0x1.62e42ep6f", "-0x1.9fe368p6f"):
+        assert c in body, c
+    assert "glibc_expf(mul_rn(-ax, ax))" in src

@@ -278,8 +278,51 @@ __device__ __forceinline__ float gelu_fast_form(float v) {
     return (0.5f * v) * (1.0f + erf);
 }
 
+// expf as glibc 2.35 computes it on x86-64 with FMA (the function the
+// crate's f32::exp calls on Linux), so that the scalar GELU below gives the
+// crate's bits.  The published design of that expf (ARM optimized-routines,
+// taken into glibc 2.27): x * 32/ln2 = k + r with k rounded to an integer by
+// the 1.5 * 2^52 shift, 2^(k/32) from a 32-entry table of the correctly
+// rounded 2^(i/32) with i << 47 subtracted from each entry's bits (so that
+// adding k << 47 puts k / 32 into the exponent), and 2^(r/32) by a degree-3
+// polynomial, all in double, every multiply-add fused, then one rounding to
+// float.  Reproduced exactly, this form equals the host libm's expf for all
+// 2^32 inputs (an exhaustive host comparison of the same arithmetic in the
+// test suite); the device's own expf is within 1 ulp but not always equal.
+__device__ __forceinline__ float glibc_expf(float x) {
+    constexpr uint64_t kTab[32] = {
+        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+    const uint32_t bits = __builtin_bit_cast(uint32_t, x);
+    const uint32_t abstop = (bits >> 20) & 0x7ff;
+    if (abstop >= 0x42b) {                            // |x| >= 88, inf or NaN
+        if (bits == 0xff800000u) return 0.0f;          // exp(-inf)
+        if (abstop >= 0x7f8) return x + x;             // +inf, NaN
+        if (x > 0x1.62e42ep6f) return __builtin_inff(); // overflow
+        if (x < -0x1.9fe368p6f) return 0.0f;           // underflow
+    }
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_n, xd, shift);
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    const double s = __builtin_bit_cast(double, kTab[ki % 32] + (ki << 47));
+    const double z = __builtin_fma(c0, r, c1), r2 = r * r;
+    const double y = __builtin_fma(z, r2, __builtin_fma(c2, r, 1.0));
+    return (float)(y * s);
+}
+
 // Scalar GELU of src/scalar.rs:116-134 (used by the AVX-512 path's n%16
-// tail); expf is the device libm's, within 1 ulp of glibc's.
+// tail), with the host libm's expf (glibc_expf above).
 __device__ __forceinline__ float gelu_scalar_form(float v) {
     float x = mul_rn(v, 0.70710677f);
     float s = isnan(x) ? x : copysignf(1.0f, x);
@@ -289,7 +332,7 @@ __device__ __forceinline__ float gelu_scalar_form(float v) {
     p = add_rn(mul_rn(p, t), 1.4214137f);
     p = sub_rn(mul_rn(p, t), 0.28449674f);
     p = add_rn(mul_rn(p, t), 0.2548296f);
-    float y = sub_rn(1.0f, mul_rn(mul_rn(p, t), expf(mul_rn(-ax, ax))));
+    float y = sub_rn(1.0f, mul_rn(mul_rn(p, t), glibc_expf(mul_rn(-ax, ax))));
     return mul_rn(mul_rn(0.5f, v), add_rn(1.0f, mul_rn(s, y)));
 }
 
