@@ -15,15 +15,22 @@ exercised with its neighbours.  Bars:
 - the Q8_0 GEMM (Kernels::gemm_q8_0, src/dispatch.rs:91-105) bit for bit
   against the oracle, and the Q8_0 projections (bias, LayerScale, GELU,
   residual) bit for bit against the oracle's composition of the engine's
-  passes.
+  passes;
+- the elementwise and DPT operations at random sizes against the oracle:
+  Kernels::gelu, the CPU-order LayerNorm, quantize_row_q8_0, 2-D RoPE with
+  head dims 16 to 128 and the resizes bit for bit, the two-pass LayerNorm
+  within 1e-5, convolutions (any kernel size, stride and padding) and
+  transposed convolutions within twice the f32 accumulation bound of the
+  direct definition, bit for bit where the gather form applies.
 """
 import numpy as np
 import pytest
 from scipy.special import erf
 
 import oracle as O
-from conftest import assert_bits_equal
+from conftest import assert_bits_equal, max_rel
 from q8_compose import q8_linear, weight_blocks
+from vestra_hip import da3
 
 pytestmark = pytest.mark.gpu
 
@@ -49,6 +56,9 @@ Q8_LINEAR_CASES = [(str(_RNG.choice(["store", "gelu", "residual"])), _dim(1, 150
                     int(_RNG.integers(1, 1 << 30))) for _ in range(10)]
 Q8_CASES = [(_dim(1, 2000), _dim(1, 2100), 32 * int(_RNG.integers(1, 80)),
              int(_RNG.integers(1, 1 << 30))) for _ in range(12)]
+ELEMENTWISE_CASES = [(str(op), int(_RNG.integers(1, 1 << 30)))
+                     for op in _RNG.permutation(["gelu", "layernorm", "quantize", "rope", "resize",
+                                                 "conv", "conv_transpose"] * 3)]
 
 
 @pytest.mark.parametrize("mode, m, k, n, gamma, seed", PROJ_CASES)
@@ -127,3 +137,80 @@ def test_q8_linear_random_shapes_bit_exact(rt, mode, m, k, n, gamma, seed):
         got = rt.download_f32(lin.run_gelu(xt, m) if mode == "gelu" else lin.run(xt, m))
         exp = q8_linear(x, m, k, n, wb, bias, g, mode)
     assert_bits_equal(got, exp, f"Q8_0 linear {mode} {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("op, seed", ELEMENTWISE_CASES)
+def test_elementwise_random_shapes_vs_oracle(rt, op, seed):
+    rng = np.random.default_rng(seed)
+    if op == "gelu":
+        n = int(rng.integers(1, 1_000_000))
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        t = rt.upload_f32(x)
+        rt.gelu_f32_in_place(t)
+        assert_bits_equal(rt.download_f32(t), O.kernels_gelu(x), f"gelu n={n}")
+    elif op == "layernorm":
+        rows, cols = int(rng.integers(1, 3000)), int(rng.integers(1, 2100))
+        rows = max(1, min(rows, 3_000_000 // cols))
+        x = (rng.standard_normal(rows * cols) * rng.uniform(0.1, 5) + rng.uniform(-3, 3)).astype(np.float32)
+        g = (rng.standard_normal(cols) * 0.2 + 1).astype(np.float32)
+        b = (rng.standard_normal(cols) * 0.1).astype(np.float32)
+        exp = O.layernorm(x, rows, cols, g, b, 1e-6)
+        xt, gt, bt = rt.upload_f32(x), rt.upload_f32(g), rt.upload_f32(b)
+        assert max_rel(rt.download_f32(rt.layernorm_f32(xt, gt, bt, rows, cols, 1e-6)), exp) <= 1e-5
+        assert_bits_equal(rt.download_f32(rt.layernorm_f32_cpu_order(xt, gt, bt, rows, cols, 1e-6)),
+                          exp, f"cpu-order LayerNorm {rows}x{cols}")
+    elif op == "quantize":
+        rows, k = int(rng.integers(1, 5000)), 32 * int(rng.integers(1, 100))
+        rows = max(1, min(rows, 4_000_000 // k))
+        x = (rng.standard_normal(rows * k) * rng.uniform(0.001, 10)).astype(np.float32)
+        got = rt.q8_0_download(rt.quantize_q8_0(rt.upload_f32(x), rows, k))
+        assert np.array_equal(got.view(np.uint8), np.asarray(O.quantize_rows_q8_0(x, rows, k)).view(np.uint8))
+    elif op == "rope":
+        hd = int(rng.choice([16, 32, 64, 128]))
+        heads, gh, gw = int(rng.integers(1, 16)), int(rng.integers(1, 50)), int(rng.integers(1, 50))
+        n = gh * gw + 1
+        x = rng.standard_normal(heads * n * hd).astype(np.float32)
+        pos = da3.positions_yx(gh, gw)
+        t = rt.upload_f32(x)
+        rt.rope2d_f32_in_place(t, heads, n, hd, pos, 100.0)
+        assert_bits_equal(rt.download_f32(t), O.rope2d(x, heads, n, hd, pos, 100.0), f"rope hd={hd}")
+    elif op == "resize":
+        c, ih, iw = int(rng.integers(1, 64)), int(rng.integers(1, 80)), int(rng.integers(1, 80))
+        oh, ow = int(rng.integers(1, 200)), int(rng.integers(1, 200))
+        x = rng.standard_normal(c * ih * iw).astype(np.float32)
+        xt = rt.upload_f32(x)
+        assert_bits_equal(rt.download_f32(rt.bilinear_resize_f32(xt, c, ih, iw, oh, ow)),
+                          O.bilinear_resize(x, c, ih, iw, oh, ow), "half-pixel resize")
+        assert_bits_equal(rt.download_f32(rt.bilinear_resize_align_corners_f32(xt, c, ih, iw, oh, ow)),
+                          O.bilinear_resize_align_corners(x, c, ih, iw, oh, ow), "align-corners resize")
+    elif op == "conv":
+        in_c, out_c = int(rng.integers(1, 200)), int(rng.integers(1, 200))
+        kk, s = int(rng.choice([1, 3, 5])), int(rng.choice([1, 1, 2]))
+        p = int(rng.integers(0, kk // 2 + 2))
+        ih, iw = int(rng.integers(kk, 60)), int(rng.integers(kk, 60))
+        x = rng.standard_normal(in_c * ih * iw).astype(np.float32)
+        w = (rng.standard_normal(out_c * in_c * kk * kk) / np.sqrt(in_c * kk * kk)).astype(np.float32)
+        b = rng.standard_normal(out_c).astype(np.float32)
+        got = rt.download_f32(rt.prepare_conv2d_f32(in_c, out_c, kk, kk, s, p, w, b).run(
+            rt.upload_f32(x), ih, iw))
+        exp = O.conv2d_naive(x, in_c, ih, iw, w, out_c, kk, kk, s, p, b)
+        absb = O.conv2d_naive(np.abs(x), in_c, ih, iw, np.abs(w), out_c, kk, kk, s, p, np.abs(b))
+        assert np.all(np.abs(got.astype(np.float64) - exp) <=
+                      2 * (in_c * kk * kk + 2) * 6e-8 * absb.astype(np.float64) + 1e-30)
+    else:
+        in_c, out_c = int(rng.integers(1, 200)), int(rng.integers(1, 100))
+        kk = int(rng.choice([2, 3, 4, 5]))
+        s = int(rng.choice([kk, kk, 2, 3]))
+        ih, iw = int(rng.integers(1, 30)), int(rng.integers(1, 30))
+        x = rng.standard_normal(in_c * ih * iw).astype(np.float32)
+        w = (rng.standard_normal(in_c * out_c * kk * kk) / np.sqrt(in_c)).astype(np.float32)
+        b = rng.standard_normal(out_c).astype(np.float32)
+        got = rt.download_f32(rt.conv_transpose2d_f32(rt.upload_f32(x), in_c, ih, iw, w, out_c, kk,
+                                                      kk, s, b))
+        exp = O.conv_transpose2d_naive(x, in_c, ih, iw, w, out_c, kk, kk, s, b)
+        if s == kk:
+            absb = O.conv_transpose2d_naive(np.abs(x), in_c, ih, iw, np.abs(w), out_c, kk, kk, s,
+                                            np.abs(b))
+            assert np.all(np.abs(got.astype(np.float64) - exp) <= 2 * (in_c + 2) * 6e-8 * absb + 1e-30)
+        else:
+            assert_bits_equal(got, exp, f"gather transposed conv k{kk} s{s}")
