@@ -116,6 +116,7 @@ def measured_traffic(launch: str):
 
 MFMA_SUMMARY = ROOT / "profiles" / "block_865_mfma_busy.md"
 TRACE_SUMMARY = ROOT / "profiles" / "block_865_kernel_trace.md"
+CONFIG_TRACE_SUMMARY = ROOT / "profiles" / "configs_kernel_trace.md"
 
 
 def measured_trace_us() -> dict:
@@ -138,6 +139,25 @@ def measured_trace_us() -> dict:
         if in_block and len(cells) == 3 and cells[0].startswith("`"):
             try:
                 out[cells[0].strip("`")] = out.get(cells[0].strip("`"), 0.0) + float(cells[2])
+            except ValueError:
+                pass
+    return out
+
+
+def measured_config_trace_us() -> dict:
+    """Kernel-trace durations of the standalone config 1 and 2 cases from the
+    committed rocprofv3 --kernel-trace summary (median over each case's timed
+    launches), keyed by case name; {} when absent."""
+    try:
+        text = CONFIG_TRACE_SUMMARY.read_text()
+    except OSError:
+        return {}
+    out = {}
+    for line in text.splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 7 and cells[0].startswith("`"):
+            try:
+                out[cells[0].strip("`")] = float(cells[3])
             except ValueError:
                 pass
     return out
@@ -618,6 +638,7 @@ def gpu_configs(reps: int = 20) -> dict:
                       (lambda lin=lin, xt=xt: lin.run(xt, T)), "gemm_bias_scale",
                       2.0 * T * kk * nn))
     out = {}
+    traced = measured_config_trace_us()
     for label, fn, prof_name, flops in cases:
         settle = settle_clock(rt, fn)
         rt.timer_start()
@@ -638,7 +659,15 @@ def gpu_configs(reps: int = 20) -> dict:
                       "us_burst": round(us_burst, 2),
                       "frac_fp32_mfma_burst": round(tf_burst / PEAK_FP32_MFMA_TFLOPS, 4),
                       "clock_settle": {"ms": CLOCK_SETTLE_MS, "launches": settle}}
+        if label in traced:
+            out[label]["trace_us"] = traced[label]
+            out[label]["frac_fp32_mfma_trace"] = round(
+                flops / (traced[label] * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)
         log(f"  {label:34s} {us:8.2f} us {tf:7.2f} TF/s per-launch events (burst {us_burst:.2f})")
+    if traced:
+        out["trace_source"] = ("profiles/configs_kernel_trace.md: committed rocprofv3 --kernel-trace "
+                               "summary (median over each case's timed launches), not measured in "
+                               "this run")
     return out
 
 
