@@ -244,7 +244,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     int tile_m, tile_n, split, kbeg, kend;
     int piece = -1, tail_u = 0;
     if constexpr (TAIL) {
-        static_assert(!SPLIT && EXACT && CONV == 0, "balanced tail: plain whole-slice GEMMs");
+        static_assert(!SPLIT && EXACT && (CONV == 0 || CONV == 3),
+                      "balanced tail: whole-slice GEMMs and the direct convolution");
         if (tail_tile_of_block(ep, xcd_order != 0, (N + BN - 1) / BN, (M + BM - 1) / BM, tile_m, tile_n,
                                piece, tail_u) < 0)
             return;
@@ -1504,11 +1505,11 @@ bool tail_plan(const GemmArgs &g, const Tile &t, TailPlan *plan, int only_splits
     return true;
 }
 
-template <Epi EPI, int LNF = 0>
+template <Epi EPI, int LNF = 0, int CONV = 0>
 hipError_t launch_tail(hipStream_t s, const GemmArgs &g, EpiArgs ep, const TailPlan &p) {
     constexpr int BM = 64, BN = 64, BK = 32, WM = 2, WN = 2;
     constexpr size_t lds = gemm_lds_bytes<BM, BN, BK>();
-    auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, false, true, 0, true, LNF>;
+    auto kernel = gemm_nt_kernel<BM, BN, BK, WM, WN, EPI, false, true, CONV, true, LNF>;
     static std::atomic<uint64_t> configured{0};
     if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
     ep.partial = g.tail_ws;
@@ -1709,9 +1710,14 @@ hipError_t dispatch_conv(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
 }
 
 // Direct convolution of a CHW image: the 64 x 64 x 32 tile (one pixel and
-// 8 channels per thread in the loader).
+// 8 channels per thread in the loader), with the balanced tail when the
+// tiles leave a partial last round over the CUs (tail_plan; the DPT 3x3
+// 128 -> 128 convolution on 144 x 96: 432 tiles, the last 176 as 4 K
+// pieces).
 hipError_t dispatch_conv_direct(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
     if (g.conv_in_c % 32 != 0 || g.k % 32 != 0 || g.k == 0) return hipErrorInvalidValue;
+    TailPlan p;
+    if (tail_plan(g, Tile{64, 64, 32, 2, 2}, &p)) return launch_tail<Epi::Store, 0, 3>(s, g, ep, p);
     return launch_tile<64, 64, 32, 2, 2, Epi::Store, false, true, 3>(s, g, ep, 1, (int)g.k);
 }
 

@@ -2266,6 +2266,7 @@ vh_status conv_run(RtState &s, const vh_conv2d &c, const float *in, size_t ih, s
         g.conv_stride = c.stride;
         g.conv_pad = c.pad;
         g.conv_relu = relu;
+        TRY(tail_workspace(s, g));
         return launch(s, "conv_gemm", [&] { return vh::launch_gemm(s.stream, g); });
     }
     if (c.hwc && c.stride == 1 && c.in_c % 32 == 0 && !plain) {
