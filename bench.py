@@ -3,10 +3,10 @@
 
 Metric: "DA3-BASE ViT block us @504x336 (865 tok); GEMM/attn %
 fp32-MFMA peak".  A step is one full encoder block over a
-synthetic 865-token image already resident in HBM, as six kernels on the
+synthetic 865-token image already resident in HBM, as five kernels on the
 runtime's stream: QKV with LayerNorm 1 folded in (row statistics from its A
-slices) and RoPE; flash attention over 3 key splits; the merge of the splits;
-out-projection+LayerScale+residual (writing the updated rows' statistics);
+slices) and RoPE; flash attention over 3 key splits, merged in split order by
+the split that finishes last in each query group; out-projection+LayerScale+residual (writing the updated rows' statistics);
 fc1 with LayerNorm 2 folded in and GELU; fc2+LayerScale+residual.
 
 Timing: the block is prepared, then runs W untimed steps and K steps between

@@ -689,6 +689,33 @@ def test_flash_key_layouts_deterministic_and_consistent(rt, monkeypatch):
             assert max_rel(a, outs[("1", "1", "1")]) <= 2e-6, (H, T, key)
 
 
+@pytest.mark.parametrize("token_major", [False, True], ids=["head_major", "token_major"])
+def test_flash_in_kernel_merge_equals_merge_launch(rt, monkeypatch, token_major):
+    """Key splits merged by the split that finishes last in each 64-query
+    group (VESTRA_HIP_FLASH_FUSED=1; the default when the grid is one round
+    of workgroups) equal, bit for bit, the same splits merged by the separate
+    merge launch (=0), at 2, 3 and 4 splits, for full and partial last query
+    tiles and for grids of one round (12 x 865 at 2 and 3 splits) and of
+    several (48 x 865).  Each shape runs three times,
+    every output kept alive so that no run lands in an earlier run's memory:
+    the arrival counters must be back at zero after every run, or a later
+    run would merge early or leave rows unwritten."""
+    for H, T in ((12, 865), (48, 865), (1, 130), (3, 200), (2, 257)):
+        n = H * T * 64
+        q, k, v = (rt.upload_f32(seeded.normal(s + 7 * T + H, n)) for s in (41, 42, 43))
+        for splits in ("2", "3", "4"):
+            monkeypatch.setenv("VESTRA_HIP_FLASH_SPLITS", splits)
+            monkeypatch.setenv("VESTRA_HIP_FLASH_FUSED", "0")
+            exp = rt.download_f32(rt.flash_attention_f32_da3_base(q, k, v, H, T, token_major))
+            assert np.isfinite(exp).all()
+            monkeypatch.setenv("VESTRA_HIP_FLASH_FUSED", "1")
+            kept = []
+            for run in range(3):
+                kept.append(rt.flash_attention_f32_da3_base(q, k, v, H, T, token_major))
+                assert_bits_equal(rt.download_f32(kept[-1]), exp,
+                                  f"in-kernel merge {H}x{T} splits={splits} run {run}")
+
+
 # ---- streaming forms (launches that move >= 128 MiB) --------------------------
 # Past 128 MiB of traffic the elementwise kernels switch to non-temporal
 # loads and stores with more bytes in flight per thread.  Only the access

@@ -55,7 +55,63 @@ struct FlashArgs {
     // output rows as block-major Q8_0 (quantize_row_q8_0) instead of f32.
     int8_t *q8_qs;
     uint16_t *q8_d;
+    // Fused merge (flash_direct_kernel<.., FUSED>): the splits of query
+    // group g = bh * qtiles + qt publish thread-major partials at
+    // pt + (g * splits + z) * kFusedPartial (16 output values per thread,
+    // then m and l of the thread's query), and cnt[g] counts them in; it is
+    // zero on entry and the split that merges leaves it zero.
+    float *pt;
+    unsigned *cnt;
 };
+constexpr int kFusedValues = 18;  // per thread: o[4][4], m, l
+constexpr size_t kFusedPartial = (size_t)kFusedValues * 256;
+
+// Stores the merged output dims d4..d4+3 of query `query` of head-row bh:
+// token-major f32, token-major block-major Q8_0 (fa.q8_qs), or head-major
+// f32.  For Q8_0 the eight consecutive lanes of a 16-lane row that hold
+// one 32-column block take its absmax with three DPP steps, so all eight
+// must be active.
+template <bool TOKEN_MAJOR>
+__device__ __forceinline__ void store_merged(const FlashArgs &fa, int bh, int query, int d4, f32x4 o) {
+    float *dst;
+    if constexpr (TOKEN_MAJOR) {
+        const int img = bh / fa.heads, head = bh % fa.heads;
+        if (fa.q8_qs) {
+            // Row img*T + query of the token-major [images*T][heads*64]
+            // output, quantised as quantize_row_q8_0 does.
+            float amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) amax = q8_absmax(amax, o[e]);
+            amax = q8_absmax(amax, dpp_f32<0xb1>(amax));
+            amax = q8_absmax(amax, dpp_f32<0x4e>(amax));
+            amax = q8_absmax(amax, dpp_f32<0x141>(amax));
+            float d, qinv;
+            q8_scale(amax, d, qinv);
+            uint32_t w = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float qv = roundf(mul_rn(o[e], qinv));  // f32::round: half away from zero
+                int qi;
+                if (isnan(qv)) {
+                    qi = 0;  // `NaN as i8` saturates to 0
+                } else {
+                    qv = fminf(fmaxf(qv, -127.0f), 127.0f);
+                    qi = (int)qv;
+                }
+                w |= ((uint32_t)(qi & 0xff)) << (8 * e);
+            }
+            const size_t M = (size_t)(fa.bh / fa.heads) * fa.T;
+            const size_t slot = (size_t)(head * 2 + (d4 >> 5)) * M + (size_t)img * fa.T + query;
+            reinterpret_cast<uint32_t *>(fa.q8_qs + slot * 32)[(d4 & 31) >> 2] = w;
+            if ((d4 & 31) == 0) fa.q8_d[slot] = __builtin_bit_cast(uint16_t, (_Float16)d);
+            return;
+        }
+        dst = fa.out + ((size_t)img * fa.T + query) * ((size_t)fa.heads * D) + (size_t)head * D;
+    } else {
+        dst = fa.out + ((size_t)bh * fa.T + query) * D;
+    }
+    *reinterpret_cast<f32x4 *>(dst + d4) = o;
+}
 
 // V panels are stored transposed, Vt[d][key], so that the four keys a lane
 // feeds to one PV k-step are one 16-byte read.  Key column k of row d sits
@@ -379,9 +435,13 @@ __device__ __forceinline__ float max_xor32(float v) {
     return fmaxf(a, b);
 }
 
-template <bool TOKEN_MAJOR, bool SPLIT>
+// FUSED (with SPLIT): the split that finishes last in its query group
+// merges the group's partials itself (flash_merge_kernel's arithmetic and
+// order), so no merge launch follows.
+template <bool TOKEN_MAJOR, bool SPLIT, bool FUSED = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_direct_kernel(
     FlashArgs fa) {
+    static_assert(SPLIT || !FUSED, "the fused merge is for key splits");
     extern __shared__ __attribute__((aligned(16))) float smem[];
     float *Ks = smem;              // [2][64 keys][64], swizzled granules
     float *Vs = smem + 2 * PANEL;  // [2][64 keys][64]
@@ -532,6 +592,78 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
+    if constexpr (FUSED) {
+        // Publish this split's partial thread-major (each store instruction
+        // writes 256 consecutive bytes per wave), then count it in; the
+        // split that sees the last count merges.  Ordering as in the GEMM's
+        // balanced tail: agent-scope atomic stores write through the XCD's
+        // L2 to where every XCD reads; each thread waits for its stores'
+        // acknowledgement (vmcnt counts stores; inline asm with a memory
+        // clobber, so no store moves past it); the barrier orders those
+        // waits before thread 0's agent-scope increment; the merging split
+        // reads with agent-scope atomic loads, which bypass the L2.  No
+        // split waits for another, so the grid drains at any residency.
+        const int group = bh * fa.qtiles + qt;
+        const float *grp = fa.pt + (size_t)group * fa.splits * kFusedPartial + tid;
+        float *mine = fa.pt + ((size_t)group * fa.splits + z) * kFusedPartial + tid;
+#pragma unroll
+        for (int df = 0; df < 4; df++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                __hip_atomic_store(mine + (df * 4 + r) * 256, o[df][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(mine + 16 * 256, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(mine + 17 * 256, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        __shared__ int merge_here;
+        if (tid == 0)
+            merge_here = __hip_atomic_fetch_add(fa.cnt + group, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                         (unsigned)(fa.splits - 1);
+        __syncthreads();
+        if (!merge_here) return;
+        // Every split's values (this one's too) are loaded before the first
+        // use, under a uniform branch per split.
+        float pv[kMaxFlashSplits][kFusedValues];
+#pragma unroll
+        for (int p = 0; p < kMaxFlashSplits; p++) {
+#pragma unroll
+            for (int e = 0; e < kFusedValues; e++)
+                pv[p][e] = p < fa.splits ? __hip_atomic_load(grp + (p * kFusedValues + e) * 256, __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_AGENT)
+                                         : 0.0f;
+        }
+        if (tid == 0) __hip_atomic_store(fa.cnt + group, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // Split weights and inverse sum of this lane's query li, then of
+        // each output row (query qw + 4lh + r, held by lane 4lh + r).
+        float mm = pv[0][16];
+#pragma unroll
+        for (int p = 1; p < kMaxFlashSplits; p++)
+            if (p < fa.splits) mm = fmaxf(mm, pv[p][16]);
+        float w[kMaxFlashSplits], lsum = 0.0f;
+#pragma unroll
+        for (int p = 0; p < kMaxFlashSplits; p++) {
+            w[p] = 0.0f;
+            if (p < fa.splits) {
+                w[p] = __builtin_amdgcn_exp2f(pv[p][16] - mm);
+                lsum += w[p] * pv[p][17];
+            }
+        }
+        const float inv = 1.0f / lsum;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float wr[kMaxFlashSplits];
+#pragma unroll
+            for (int p = 0; p < kMaxFlashSplits; p++) wr[p] = __shfl(w[p], 4 * lh + r, 64);
+            const float ir = __shfl(inv, 4 * lh + r, 64);
+            f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int p = 0; p < kMaxFlashSplits; p++)
+                if (p < fa.splits) acc += wr[p] * f32x4{pv[p][r], pv[p][4 + r], pv[p][8 + r], pv[p][12 + r]};
+            const int qr = qw + 4 * lh + r;
+            if (qr < T) store_merged<TOKEN_MAJOR>(fa, bh, qr, 4 * li, acc * ir);
+        }
+        return;
+    }
     // Output row r of this lane is query qw + 4lh + r, whose (m, l) sit in
     // lane 4lh + r.
     float lr[4], mr[4];
@@ -564,7 +696,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 // Combines the key splits of each (head, query) in split order:
 // O = sum_z 2^(m_z - M) o_z / sum_z 2^(m_z - M) l_z with M = max_z m_z.
-// One thread per four output dims; all reads are issued first.
+// One thread per four output dims; all reads are issued first.  The fused
+// form inside flash_direct_kernel does the same arithmetic in the same order.
 template <bool TOKEN_MAJOR, int S>
 __global__ __launch_bounds__(256) void flash_merge_kernel(FlashArgs fa) {
     const size_t rows = (size_t)fa.bh * fa.T;
@@ -591,47 +724,7 @@ __global__ __launch_bounds__(256) void flash_merge_kernel(FlashArgs fa) {
         acc += w * po[z];
     }
     const float inv = 1.0f / lsum;
-    const f32x4 o = acc * inv;
-    float *dst;
-    if constexpr (TOKEN_MAJOR) {
-        const int bh = (int)(row / fa.T), query = (int)(row % fa.T);
-        const int img = bh / fa.heads, head = bh % fa.heads;
-        if (fa.q8_qs) {
-            // Row img*T + query of the token-major [images*T][heads*64]
-            // output; a 32-column block is eight adjacent threads (d4 / 4 of
-            // one half of a head row), whose max takes three DPP steps.
-            float amax = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 4; e++) amax = q8_absmax(amax, o[e]);
-            amax = q8_absmax(amax, dpp_f32<0xb1>(amax));
-            amax = q8_absmax(amax, dpp_f32<0x4e>(amax));
-            amax = q8_absmax(amax, dpp_f32<0x141>(amax));
-            float d, qinv;
-            q8_scale(amax, d, qinv);
-            uint32_t w = 0;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float qv = roundf(mul_rn(o[e], qinv));  // f32::round: half away from zero
-                int qi;
-                if (isnan(qv)) {
-                    qi = 0;  // `NaN as i8` saturates to 0
-                } else {
-                    qv = fminf(fmaxf(qv, -127.0f), 127.0f);
-                    qi = (int)qv;
-                }
-                w |= ((uint32_t)(qi & 0xff)) << (8 * e);
-            }
-            const size_t M = (size_t)(fa.bh / fa.heads) * fa.T;
-            const size_t slot = (size_t)(head * 2 + (d4 >> 5)) * M + (size_t)img * fa.T + query;
-            reinterpret_cast<uint32_t *>(fa.q8_qs + slot * 32)[(d4 & 31) >> 2] = w;
-            if ((d4 & 31) == 0) fa.q8_d[slot] = __builtin_bit_cast(uint16_t, (_Float16)d);
-            return;
-        }
-        dst = fa.out + ((size_t)img * fa.T + query) * ((size_t)fa.heads * D) + (size_t)head * D;
-    } else {
-        dst = fa.out + row * D;
-    }
-    *reinterpret_cast<f32x4 *>(dst + d4) = o;
+    store_merged<TOKEN_MAJOR>(fa, (int)(row / fa.T), (int)(row % fa.T), d4, acc * inv);
 }
 
 template <bool TOKEN_MAJOR, int KVS, bool SPLIT>
@@ -654,16 +747,16 @@ hipError_t run_flash(hipStream_t s, const FlashArgs &fa) {
     return hipGetLastError();
 }
 
-template <bool TOKEN_MAJOR, bool SPLIT>
+template <bool TOKEN_MAJOR, bool SPLIT, bool FUSED = false>
 hipError_t run_flash_direct(hipStream_t s, const FlashArgs &fa) {
     constexpr size_t lds = 2 * (size_t)(2 * PANEL) * sizeof(float);
-    auto kernel = flash_direct_kernel<TOKEN_MAJOR, SPLIT>;
+    auto kernel = flash_direct_kernel<TOKEN_MAJOR, SPLIT, FUSED>;
     static std::atomic<uint64_t> configured{0};
     if (hipError_t e = ensure_dynamic_lds(kernel, lds, configured); e != hipSuccess) return e;
     const int total = fa.bh * fa.qtiles * (SPLIT ? fa.splits : 1);
     const int grid = fa.xcd_map ? (total + 7) / 8 * 8 : total;
     kernel<<<grid, 256, lds, s>>>(fa);
-    if constexpr (SPLIT) {
+    if constexpr (SPLIT && !FUSED) {
         const size_t threads = (size_t)fa.bh * fa.T * 16;
         const dim3 mgrid((unsigned)((threads + 255) / 256));
         if (fa.splits == 2) flash_merge_kernel<TOKEN_MAJOR, 2><<<mgrid, 256, 0, s>>>(fa);
@@ -717,10 +810,17 @@ size_t flash_workspace_floats(size_t bh, size_t tokens) {
     return (size_t)kMaxFlashSplits * bh * tokens * (D + 2);
 }
 
+size_t flash_fused_workspace_floats(size_t bh, size_t tokens) {
+    return (size_t)kMaxFlashSplits * flash_query_groups(bh, tokens) * kFusedPartial;
+}
+
+size_t flash_query_groups(size_t bh, size_t tokens) { return bh * ((tokens + BQ - 1) / BQ); }
+
 hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k, const float *v,
                                   float *out, size_t bh, size_t tokens, size_t heads,
                                   bool token_major, float *ws, size_t ws_floats, int8_t *q8_qs,
-                                  uint16_t *q8_d, bool *quantized, float softmax_scale) {
+                                  uint16_t *q8_d, bool *quantized, float softmax_scale,
+                                  unsigned *cnt, size_t cnt_n) {
     if (quantized) *quantized = false;
     if (bh == 0 || tokens == 0) return hipSuccess;
     FlashArgs fa{};
@@ -787,6 +887,26 @@ hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k,
             fa.q8_qs = q8_qs;
             fa.q8_d = q8_d;
             if (quantized) *quantized = true;
+        }
+        // The last split of each query group merges in the kernel when the
+        // caller gives the arrival counters and room for the thread-major
+        // partials, and the grid is one round of workgroups (two per CU):
+        // then every group's last split merges at the very end, where the
+        // merge launch would add its own launch and first-load latency
+        // (block at 865 tokens 152.5 -> 151.9 us).  Over several rounds the
+        // merge launch is faster: it reads partials the L2 still holds,
+        // where the in-kernel merge writes them through and reads them back
+        // (12-layer encoder at 4 x 865 tokens 6.13 against 6.21 ms).
+        // VESTRA_HIP_FLASH_FUSED=0 / 1 turns it off / on whenever possible.
+        bool fused = direct && cnt != nullptr && cnt_n >= (size_t)items &&
+                     ws_floats >= (size_t)splits * items * kFusedPartial;
+        if (const char *e = std::getenv("VESTRA_HIP_FLASH_FUSED")) fused = fused && std::atoi(e) != 0;
+        else fused = fused && items * splits <= 512;
+        if (fused) {
+            fa.pt = ws;
+            fa.cnt = cnt;
+            return token_major ? run_flash_direct<true, true, true>(s, fa)
+                               : run_flash_direct<false, true, true>(s, fa);
         }
         if (direct)
             return token_major ? run_flash_direct<true, true>(s, fa) : run_flash_direct<false, true>(s, fa);

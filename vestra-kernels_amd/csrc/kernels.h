@@ -61,6 +61,12 @@ hipError_t launch_unpad_rows(hipStream_t s, const float *src, float *dst, size_t
 // floats; with ws == nullptr (or too small) the kernel runs unsplit.
 constexpr int kMaxFlashSplits = 4;
 size_t flash_workspace_floats(size_t bh, size_t tokens);
+// With cnt (flash_query_groups() counters, zero on entry, left zero) and a
+// workspace of flash_fused_workspace_floats() floats, the split that ends
+// last in each 64-query group merges the group in the kernel (bit-identical
+// to the merge launch that runs otherwise).
+size_t flash_query_groups(size_t bh, size_t tokens);
+size_t flash_fused_workspace_floats(size_t bh, size_t tokens);
 // With q8_qs / q8_d (token-major only) a run that splits the keys writes its
 // output as block-major Q8_0 rows [images*tokens][heads*64] from the merge
 // (bit-identical to the f32 output quantised) and sets *quantized; otherwise
@@ -69,7 +75,8 @@ hipError_t launch_flash_attention(hipStream_t s, const float *q, const float *k,
                                   float *out, size_t bh, size_t tokens, size_t heads,
                                   bool token_major, float *ws, size_t ws_floats,
                                   int8_t *q8_qs = nullptr, uint16_t *q8_d = nullptr,
-                                  bool *quantized = nullptr, float softmax_scale = 0.125f);
+                                  bool *quantized = nullptr, float softmax_scale = 0.125f,
+                                  unsigned *cnt = nullptr, size_t cnt_n = 0);
 
 // ---- DPT head (k_dpt.hip) ------------------------------------------------
 // colT [oh*ow][in_c*kh*kw] of a CHW input (zero padding; ReLU on the input

@@ -87,6 +87,8 @@ struct RtState {
     size_t sk_floats = 0;
     float *fw = nullptr;                        // grow-only attention key-split partials
     size_t fw_floats = 0;
+    unsigned *fcnt = nullptr;                   // and the in-kernel merge's arrival counters
+    size_t fcnt_n = 0;
     char *aq = nullptr;                         // grow-only Q8_0 activation blocks
     size_t aq_bytes = 0;
     float *tw = nullptr;                        // balanced-tail GEMM partials
@@ -106,6 +108,7 @@ struct RtState {
         if (ws) hipFree(ws);
         if (sk) hipFree(sk);
         if (fw) hipFree(fw);
+        if (fcnt) hipFree(fcnt);
         if (aq) hipFree(aq);
         if (tw) hipFree(tw);
         if (tcnt) hipFree(tcnt);
@@ -414,8 +417,10 @@ bool flash_grid_fits(size_t heads, size_t tokens) {
 vh_status flash(RtState &s, const float *q, const float *k, const float *v, float *out,
                 size_t bh, size_t tokens, size_t heads, bool token_major, int8_t *q8_qs = nullptr,
                 uint16_t *q8_d = nullptr, bool *quantized = nullptr, float scale = 0.125f) {
-    // Partials of the key splits; without them the kernel runs unsplit.
-    const size_t need = vh::flash_workspace_floats(bh, tokens);
+    // Partials of the key splits (room for either layout: the merge launch's
+    // or the in-kernel merge's); without them the kernel runs unsplit.
+    const size_t need =
+        std::max(vh::flash_workspace_floats(bh, tokens), vh::flash_fused_workspace_floats(bh, tokens));
     if (s.fw_floats < need) {
         hipStreamSynchronize(s.stream);
         if (s.fw) hipFree(s.fw);
@@ -424,9 +429,28 @@ vh_status flash(RtState &s, const float *q, const float *k, const float *v, floa
         if (hipMalloc(&s.fw, need * sizeof(float)) == hipSuccess) s.fw_floats = need;
         else hipGetLastError();
     }
+    // Arrival counters of the in-kernel merge, zeroed once here (outside any
+    // stream capture: the first run of a shape allocates); every run leaves
+    // them zero.  Without them the merge runs as its own launch.
+    const size_t groups = vh::flash_query_groups(bh, tokens);
+    if (s.fcnt_n < groups) {
+        hipStreamSynchronize(s.stream);
+        if (s.fcnt) hipFree(s.fcnt);
+        s.fcnt = nullptr;
+        s.fcnt_n = 0;
+        if (hipMalloc(&s.fcnt, groups * sizeof(unsigned)) == hipSuccess &&
+            hipMemsetAsync(s.fcnt, 0, groups * sizeof(unsigned), s.stream) == hipSuccess) {
+            s.fcnt_n = groups;
+        } else {
+            hipGetLastError();
+            if (s.fcnt) hipFree(s.fcnt);
+            s.fcnt = nullptr;
+        }
+    }
     return launch(s, "flash_attention", [&] {
         return vh::launch_flash_attention(s.stream, q, k, v, out, bh, tokens, heads, token_major,
-                                          s.fw, s.fw_floats, q8_qs, q8_d, quantized, scale);
+                                          s.fw, s.fw_floats, q8_qs, q8_d, quantized, scale, s.fcnt,
+                                          s.fcnt_n);
     });
 }
 
