@@ -166,6 +166,23 @@ def test_conv_transpose_nonoverlap_vs_naive(rt, in_c, out_c, ih, iw, k):
     assert np.abs(got - ref_main).max() < 1e-4
 
 
+@pytest.mark.parametrize("in_c, out_c, ih, iw, k", [
+    (96, 96, 24, 36, 4), (192, 192, 24, 36, 2), (32, 5, 7, 9, 4), (32, 7, 4, 5, 3)])
+def test_conv_transpose_chw_read_equals_channel_last_copy(rt, monkeypatch, in_c, out_c, ih, iw, k):
+    """The patch-scatter GEMM reading the CHW input in place (the default)
+    against the same GEMM over a channel-last copy (VESTRA_HIP_CONV_DIRECT=0):
+    the same products in the same k order, so the same bits, including the
+    partial last pixel tile (63 and 20 pixels)."""
+    x, w, b = _data(0xC7A0 + in_c + k, in_c * ih * iw, in_c * out_c * k * k, out_c)
+    ct = rt.prepare_conv_transpose2d_f32(in_c, out_c, k, k, k, w, b)
+    xt = rt.upload_f32(x)
+    monkeypatch.setenv("VESTRA_HIP_CONV_DIRECT", "0")
+    staged = rt.download_f32(ct.run(xt, ih, iw))
+    monkeypatch.setenv("VESTRA_HIP_CONV_DIRECT", "1")
+    direct = rt.download_f32(ct.run(xt, ih, iw))
+    assert_bits_equal(direct, staged, f"transposed conv {in_c}->{out_c} k{k} from CHW")
+
+
 def test_conv_transpose_k4s4_hand_checked(rt):
     """src/conv.rs:1248-1296."""
     w = np.zeros(64, np.float32)

@@ -209,7 +209,9 @@ constexpr size_t gemm_lds_bytes() {
 // [out_c][K], so the output tile is channel-major and is written straight to
 // the CHW output.  CONV == 2 (EXACT only) is a plain GEMM whose tile rows
 // are (out channel, tap) and columns input pixels, stored by the patch
-// scatter of EpiArgs.  CONV == 3 (EXACT only) reads the Bt tile straight
+// scatter of EpiArgs; CONV == 4 is the same GEMM with Bt read as CONV == 3
+// reads it (a 1 x 1 tap over the CHW input, no transposed copy).  CONV == 3
+// (EXACT only) reads the Bt tile straight
 // from a CHW image: a thread owns one output pixel of the tile and 8
 // channels of the k-slice, so 64 lanes load 64 consecutive pixels of one
 // channel; taps outside the image load a clamped in-range pixel and are
@@ -265,7 +267,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
     // the prefetched slice lies inside the image.
     int cd_p = 0, cd_cg = 0, cd_y = 0, cd_x = 0;
     bool cd_live = false, cd_ok = false;
-    if constexpr (CONV == 3) {
+    if constexpr (CONV == 3 || CONV == 4) {
         static_assert(BN * BK == 8 * NT && NT % BN == 0 && BCH == 2,
                       "direct convolution: one pixel x 8 channels per thread");
         cd_p = tid % BN;
@@ -334,7 +336,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                     Bt + ((size_t)min(n0 + row, N - 1) + shift) * ep.conv_in_c + kin + kq);
             }
             return;
-        } else if constexpr (EXACT && CONV == 3) {
+        } else if constexpr (EXACT && (CONV == 3 || CONV == 4)) {
             const int tap = k0 / ep.conv_in_c, kin = k0 - tap * ep.conv_in_c;
             const int ky = tap / ep.conv_kw, kx = tap - ky * ep.conv_kw;
             const int yi = cd_y + ky, xi = cd_x + kx;
@@ -394,7 +396,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
             int c = tid + i * NT;
             *reinterpret_cast<f32x4 *>(&as[swz<BK>(c / CPR, c % CPR)]) = ra[i];
         }
-        if constexpr (CONV == 3) {
+        if constexpr (CONV == 3 || CONV == 4) {
             // Pixel cd_p, channels 8 cd_cg .. +7 of the slice: ReLU on the
             // image values when asked, zeros for taps outside the image.
 #pragma unroll
@@ -736,7 +738,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const float *__res
                     if (row < M) part[(size_t)row * N + col] = acc[i][j][r];
                 }
         }
-    } else if constexpr (CONV == 2) {
+    } else if constexpr (CONV == 2 || CONV == 4) {
         // Row m = (oc, ky, kx), column n = input pixel (iy, ix): the output
         // element (oc, iy * kh + ky, ix * kw + kx).  A lane's four rows 4lh..
         // 4lh+3 are kx = 0..3 of one (oc, ky) when kw == 4 (rows are aligned to
@@ -1725,6 +1727,7 @@ hipError_t dispatch_conv_direct(hipStream_t s, const GemmArgs &g, const EpiArgs 
 // row count (out_c * kh * kw) and the pixel count are both moderate.
 hipError_t dispatch_scatter(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
     if (g.k % 32 != 0 || g.k == 0) return hipErrorInvalidValue;
+    if (g.scatter_chw) return launch_tile<64, 64, 32, 2, 2, Epi::Store, false, true, 4>(s, g, ep, 1, (int)g.k);
     return launch_tile<64, 64, 32, 2, 2, Epi::Store, false, true, 2>(s, g, ep, 1, (int)g.k);
 }
 
@@ -1822,6 +1825,18 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs &g) {
         ep.scat_kh = (int)g.scatter_kh;
         ep.scat_kw = (int)g.scatter_kw;
         ep.scat_iw = (int)g.scatter_iw;
+        if (g.scatter_chw) {
+            // The direct loader as a 1 x 1 convolution over the CHW input:
+            // column n is input pixel (n / iw, n % iw), channel k its row.
+            ep.conv_in_c = (int)g.k;
+            ep.conv_kw = 1;
+            ep.conv_ow = (int)g.scatter_iw;
+            ep.cd_ih = (int)(g.n / g.scatter_iw);
+            ep.cd_iw = (int)g.scatter_iw;
+            ep.cd_stride = 1;
+            ep.cd_pad = 0;
+            ep.cd_relu = 0;
+        }
         return dispatch_scatter(s, g, ep);
     }
     switch (g.epi) {

@@ -184,8 +184,10 @@ struct GemmArgs {
     // only, k % 32 == 0): a is the weight [out_c * kh * kw][k], bt the
     // channel-last input [ih * iw][k] (n = ih * iw), and C[(oc * kh + ky) * kw
     // + kx][iy * iw + ix] + bias[row] goes to the CHW output
-    // c[oc][iy * kh + ky][ix * kw + kx].
+    // c[oc][iy * kh + ky][ix * kw + kx].  With scatter_chw, bt is the CHW
+    // input [k][ih * iw] itself, read in place (no channel-last copy).
     size_t scatter_kh = 0, scatter_kw = 0, scatter_iw = 0;
+    bool scatter_chw = false;
 };
 hipError_t launch_gemm(hipStream_t s, const GemmArgs &g);
 // Sizes of the balanced-tail workspace (GemmArgs::tail_ws / tail_cnt).

@@ -2514,19 +2514,26 @@ vh_status conv_t_new(const vh_conv_transpose2d *c, const vh_tensor *input, size_
     TRY(new_tensor(c->rt, olen, &t, "conv_transpose2d output allocation"));
     vh_status st = VH_OK;
     if (c->nonoverlap && c->in_c % 32 == 0) {
-        // Channel-last input, then one GEMM with the weight rows (oc, ky, kx)
-        // as the tile rows, stored straight to CHW by its patch-scatter
-        // epilogue.
+        // One GEMM with the weight rows (oc, ky, kx) as the tile rows and the
+        // input pixels as its columns, read from the CHW input in place,
+        // stored straight to CHW by its patch-scatter epilogue.
+        // VESTRA_HIP_CONV_DIRECT=0 reads a channel-last copy instead (A/B
+        // runs; the same products in the same order, so the same bits).
+        const char *direct_env = std::getenv("VESTRA_HIP_CONV_DIRECT");
+        const bool direct = !(direct_env && direct_env[0] == '0');
         float *xt = nullptr;
-        st = dalloc(s, plane * c->in_c, &xt, "conv_transpose2d staging allocation");
-        if (!st)
-            st = launch(s, "conv_transpose_to_hwc", [&] {
-                return vh::launch_transpose(s.stream, input->ptr, xt, c->in_c, plane);
-            });
+        if (!direct) {
+            st = dalloc(s, plane * c->in_c, &xt, "conv_transpose2d staging allocation");
+            if (!st)
+                st = launch(s, "conv_transpose_to_hwc", [&] {
+                    return vh::launch_transpose(s.stream, input->ptr, xt, c->in_c, plane);
+                });
+        }
         if (!st) {
             vh::GemmArgs g{};
             g.a = c->w;
-            g.bt = xt;
+            g.bt = direct ? input->ptr : xt;
+            g.scatter_chw = direct;
             g.m = c->out_c * c->kh * c->kw;
             g.n = plane;
             g.k = c->in_c;
