@@ -43,6 +43,8 @@ CONV_CASES = [
     (96, 128, 24, 36, 3, 1, 1),      # DPT layer_rn at the 24 x 36 grid
     (768, 96, 24, 36, 1, 1, 0),      # DPT projection
     (768, 768, 24, 36, 3, 2, 1),     # DPT resize layer 4 (3x3, stride 2)
+    (768, 128, 12, 18, 3, 1, 1),     # DPT layer_rn at 12 x 18: 8 tiles, K split 27 ways
+    (384, 128, 24, 36, 3, 1, 1),     # DPT layer_rn at 24 x 36: 28 tiles, K split 9 ways
     (64, 32, 48, 72, 3, 1, 1),       # head convolution
     (3, 4, 10, 11, 5, 3, 2),
     (32, 16, 9, 11, 5, 1, 2),        # implicit GEMM, 5x5 taps, 4 junk columns per row

@@ -1232,6 +1232,22 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(int splits, int M, i
     }
 }
 
+// Split-K of the direct convolution: C = the split-order sum of the
+// partials [splits][M][N] plus the bias of row m (the output channel),
+// stored to c[m * N + n] (the CHW output).
+__global__ __launch_bounds__(256) void conv_splitk_reduce_kernel(int splits, int M, int N,
+                                                                 const float *__restrict__ part,
+                                                                 const float *__restrict__ bias,
+                                                                 float *__restrict__ c) {
+    const size_t mn = (size_t)M * N;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= mn) return;
+    float v = part[idx];
+    for (int sp = 1; sp < splits; sp++) v = add_rn(v, part[(size_t)sp * mn + idx]);
+    if (bias) v = add_rn(v, bias[idx / N]);
+    c[idx] = v;
+}
+
 // splitk_reduce_kernel for 2-4 splits and N % 4 == 0: one float4 of outputs
 // per thread, every read (partials, bias, gamma, residual) issued before the
 // arithmetic.  Per element exactly epilogue_store<EPI> of the split-order sum.
@@ -1718,6 +1734,32 @@ hipError_t dispatch_conv(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
 // pieces).
 hipError_t dispatch_conv_direct(hipStream_t s, const GemmArgs &g, const EpiArgs &ep) {
     if (g.conv_in_c % 32 != 0 || g.k % 32 != 0 || g.k == 0) return hipErrorInvalidValue;
+    // Grids of fewer than a quarter as many tiles as CUs (small outputs,
+    // long K: 768 -> 128 over 12 x 18 is 8 tiles of K = 6912) split K over
+    // up to CUs / tiles workgroups of at least 4 slices, into the
+    // balanced tail's workspace (at most CUs x 64 x 64 floats), and a second
+    // launch sums the splits in order and adds the bias; the tail's 4 pieces
+    // would leave most CUs idle.
+    // VESTRA_HIP_GEMM_TAIL=0 keeps every tile whole (A/B runs and tests).
+    const char *tail_env = std::getenv("VESTRA_HIP_GEMM_TAIL");
+    const long cus = cu_count();
+    const long tiles = (long)((g.m + 63) / 64) * (long)((g.n + 63) / 64);
+    const long ks = (long)(g.k / 32);
+    if (!(tail_env && tail_env[0] == '0') && cus > 0 && g.tail_ws && tiles * 4 < cus) {
+        long sp = std::min(cus / tiles, ks / 4);
+        while (sp > 4 && ks % sp != 0) sp--;
+        if (sp > 4 && (size_t)sp * g.m * g.n <= g.tail_ws_floats) {
+            EpiArgs e2 = ep;
+            e2.partial = g.tail_ws;
+            hipError_t e = launch_tile<64, 64, 32, 2, 2, Epi::Store, true, true, 3>(s, g, e2, (int)sp,
+                                                                                   (int)(g.k / sp));
+            if (e != hipSuccess) return e;
+            const size_t mn = g.m * g.n;
+            conv_splitk_reduce_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(
+                (int)sp, (int)g.m, (int)g.n, g.tail_ws, ep.bias, ep.c);
+            return hipGetLastError();
+        }
+    }
     TailPlan p;
     if (tail_plan(g, Tile{64, 64, 32, 2, 2}, &p)) return launch_tail<Epi::Store, 0, 3>(s, g, ep, p);
     return launch_tile<64, 64, 32, 2, 2, Epi::Store, false, true, 3>(s, g, ep, 1, (int)g.k);

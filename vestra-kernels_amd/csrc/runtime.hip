@@ -2260,14 +2260,17 @@ vh_status conv_run(RtState &s, const vh_conv2d &c, const float *in, size_t ih, s
     vh_status st = VH_OK;
     // The direct form reads the image with eight 4-byte loads per thread and
     // k-slice where the staged GEMM issues two 16-byte ones, but saves the
-    // staging launches and copies.  Measured on MI355X it wins for 1x1
-    // convolutions and for stride-1 ones up to K = 1152 and 4 M outputs
-    // (e.g. 128 -> 128 3x3 on 144 x 96: 64 vs 70 us per call); larger ones,
-    // and the strided ones that need split-K to fill the GPU, stay staged.
+    // staging launches and copies, and its balanced tail splits the K of
+    // grids too small to fill the GPU.  Measured on MI355X (3x3, per call,
+    // direct against staged): 128 -> 128 on 96 x 144 48.6 vs 74.9 us, 768 ->
+    // 128 on 12 x 18 48.4 vs 235.7, 384 -> 128 on 24 x 36 27.9 vs 124.3,
+    // 768 -> 768 stride 2 on 24 x 36 57.4 vs 82.8, 64 -> 32 on 384 x 576
+    // 169.2 vs 173.3; only stride-1 convolutions with K >= 1152 and more than
+    // 4 M outputs stay staged (128 -> 128 on 192 x 288: 168.7 vs 160.4).
     // VESTRA_HIP_CONV_DIRECT=0|1 forces either form (A/B runs).
     const char *direct_env = std::getenv("VESTRA_HIP_CONV_DIRECT");
-    const bool direct_default = (c.kh * c.kw == 1) ||
-                                (c.stride == 1 && K <= 1152 && npix * c.out_c <= ((size_t)4 << 20));
+    const bool direct_default =
+        !(c.stride == 1 && K >= 1152 && npix * c.out_c > ((size_t)4 << 20));
     const bool direct_ok = direct_env ? std::atoi(direct_env) != 0 : direct_default;
     if (direct_ok && c.hwc && c.in_c % 32 == 0) {
         // Direct implicit GEMM: the GEMM reads the CHW image in place (taps
