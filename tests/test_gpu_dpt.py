@@ -123,7 +123,8 @@ def test_conv2d_direct_matches_staged(rt, monkeypatch, in_c, out_c, ih, iw, k, s
         assert max_rel(a, t) <= 1e-5
 
 
-@pytest.mark.parametrize("in_c", [32, 12])  # direct implicit GEMM / channel-last patch copy
+# direct implicit GEMM (256: its 8 tiles split K 18 ways) / channel-last patch copy
+@pytest.mark.parametrize("in_c", [32, 256, 12])
 def test_conv2d_relu_input_equals_materialised_relu(rt, in_c):
     """src/conv.rs:1479-1520, on the device."""
     out_c, h, w_ = 24, 18, 27
