@@ -522,8 +522,9 @@ def dpt_values(seed: int, n: int) -> np.ndarray:
 def gpu_dpt(reps: int = 20) -> dict:
     """DPT-head operations at DA3-BASE fusion shapes: a 3x3 convolution
     128 -> 128 over the 144 x 96 map (a residual conv unit), the k4s4
-    transposed convolution 96 -> 96 from the 24 x 36 patch grid, and the
-    align-corners 2x upsample of 128 channels from 72 x 48.  Per-launch HIP
+    transposed convolution 96 -> 96 from the 24 x 36 patch grid, the
+    align-corners 2x upsample of 128 channels from 72 x 48, and the 3x3
+    768 -> 128 convolution of the 12 x 18 level (timed on its own).  Per-launch HIP
     event timing; conv FLOPs are 2 * pixels * out_c * in_c * 9."""
     import vestra_hip as vh
 
@@ -554,6 +555,24 @@ def gpu_dpt(reps: int = 20) -> dict:
     prof = rt.profile_report()
     rt.profile_enable(False)
     del keep
+    # The layer_rn convolution of the 12 x 18 level (768 -> 128, 3x3): 8
+    # output tiles of K = 6912, whose K the direct route splits 27 ways.
+    sc, sh, sw = 768, 12, 18
+    xs = rt.upload_f32(dpt_values(8, sc * sh * sw))
+    convs = rt.prepare_conv2d_f32(sc, c, 3, 3, 1, 1,
+                                  dpt_values(9, c * sc * 9) * np.float32(1.0 / np.sqrt(sc * 9)),
+                                  dpt_values(10, c))
+    for _ in range(20):
+        convs.run(xs, sh, sw)
+    rt.synchronize()
+    rt.profile_reset()
+    rt.profile_enable(True)
+    keep = [convs.run(xs, sh, sw) for _ in range(reps)]
+    prof_small = rt.profile_report()
+    rt.profile_enable(False)
+    del keep
+    small_us = sum(1e3 * ms / n for n, ms in prof_small.values())
+    small_flops = 2.0 * sh * sw * c * sc * 9
 
     def us(name, per=1):
         n, ms = prof[name]
@@ -579,12 +598,16 @@ def gpu_dpt(reps: int = 20) -> dict:
         "conv_transpose_k4s4_96_24x36": {
             "us": round(t_us, 2), "parts_us": {k: round(v, 2) for k, v in t_parts.items()},
             "tflops": round(t_flops / (t_us * 1e-6) / 1e12, 2)},
+        "conv3x3_768_128_12x18": {
+            "us": round(small_us, 2), "launches": sorted(prof_small),
+            "tflops": round(small_flops / (small_us * 1e-6) / 1e12, 2)},
         "resize_align_corners_128_48x72_to_96x144": {
             "us": round(r_us, 2), "gbs": round(r_bytes / (r_us * 1e-6) / 1e9, 1),
             "frac_hbm": round(r_bytes / (r_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)},
     }
     log(f"  dpt conv3x3 {conv_us:.2f} us ({out['conv3x3_128_144x96']['tflops']} TF/s), "
-        f"transposed conv {t_us:.2f} us, resize {r_us:.2f} us")
+        f"transposed conv {t_us:.2f} us, resize {r_us:.2f} us, "
+        f"conv3x3 768->128 on 12x18 {small_us:.2f} us")
     return out
 
 

@@ -1242,8 +1242,17 @@ __global__ __launch_bounds__(256) void conv_splitk_reduce_kernel(int splits, int
     const size_t mn = (size_t)M * N;
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= mn) return;
+    // Sixteen partials in flight at a time (clamped split index, so every
+    // load is in range and none waits behind a select), added in order.
     float v = part[idx];
-    for (int sp = 1; sp < splits; sp++) v = add_rn(v, part[(size_t)sp * mn + idx]);
+    for (int base = 1; base < splits; base += 16) {
+        float t[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) t[u] = part[(size_t)min(base + u, splits - 1) * mn + idx];
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (base + u < splits) v = add_rn(v, t[u]);
+    }
     if (bias) v = add_rn(v, bias[idx / N]);
     c[idx] = v;
 }
