@@ -1212,11 +1212,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(int splits, int M, i
     if ((N & 3) == 0) {
         const f32x4 *part = reinterpret_cast<const f32x4 *>(ep.partial);
         for (size_t i4 = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i4 < mn / 4; i4 += stride) {
+            // Eight partials in flight at a time (clamped split index: every
+            // load in range, none behind a select), added in split order.
             f32x4 v = part[i4];
-            for (int s = 1; s < splits; s++) {
-                const f32x4 w = part[(size_t)s * (mn / 4) + i4];
+            for (int base = 1; base < splits; base += 8) {
+                f32x4 w[8];
 #pragma unroll
-                for (int e = 0; e < 4; e++) v[e] = add_rn(v[e], w[e]);
+                for (int u = 0; u < 8; u++) w[u] = part[(size_t)min(base + u, splits - 1) * (mn / 4) + i4];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (base + u < splits)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) v[e] = add_rn(v[e], w[u][e]);
             }
             const size_t idx = i4 * 4;
             const int col = (int)(idx % N);
@@ -1227,7 +1234,14 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(int splits, int M, i
     }
     for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < mn; idx += stride) {
         float v = ep.partial[idx];
-        for (int s = 1; s < splits; s++) v = add_rn(v, ep.partial[(size_t)s * mn + idx]);
+        for (int base = 1; base < splits; base += 8) {
+            float w[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) w[u] = ep.partial[(size_t)min(base + u, splits - 1) * mn + idx];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (base + u < splits) v = add_rn(v, w[u]);
+        }
         epilogue_store<EPI>(ep, idx, (int)(idx % N), v);
     }
 }
