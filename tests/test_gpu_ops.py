@@ -156,6 +156,36 @@ def test_gemm_row_major_matches_float64(rt, m, k, n):
     assert np.all(np.abs(c.reshape(m, n) - ref) <= bound + 1e-30)
 
 
+@pytest.mark.parametrize("rows, k, n, gamma", [(865, 768, 96, False), (864, 768, 768, False),
+                                               (37, 64, 40, False), (865, 768, 96, True),
+                                               (10, 20, 6, False)])
+def test_linear_run_chw_equals_token_to_chw_of_run(rt, monkeypatch, rows, k, n, gamma):
+    """CudaLinearF32::run_chw (src/cuda.rs:1340-1344) is token_to_chw of run.
+    A linear without LayerScale and with K % 32 == 0 computes the transposed
+    product in one GEMM (weight rows as A, input rows as Bt, channel-major
+    store); the others run, then transpose.  Against float64 within the f32
+    accumulation bound, and, with whole tiles on both routes (no balanced
+    tail), bit for bit against the composition."""
+    w = seeded.normal(7100 + n, k * n, 0.05)
+    b = seeded.normal(7200 + n, n, 0.1)
+    g = (0.5 + seeded.uniform01(7300 + n, n)).astype(np.float32) if gamma else None
+    lin = rt.prepare_linear_f32(k, n, w, b, g)
+    x = seeded.normal(7400 + rows, rows * k)
+    xt = rt.upload_f32(x)
+    got = rt.download_f32(lin.run_chw(xt, rows)).reshape(n, rows)
+    ref = x.reshape(rows, k).astype(np.float64) @ w.reshape(k, n).astype(np.float64) + b
+    if gamma:
+        ref = ref * g
+    bound = (k + 2) * 6e-8 * (np.abs(x.reshape(rows, k)).astype(np.float64) @ np.abs(w.reshape(k, n)) + np.abs(b))
+    if gamma:
+        bound = bound * np.abs(g) + 6e-8 * np.abs(ref)
+    assert np.all(np.abs(got.T - ref) <= bound + 1e-30)
+    monkeypatch.setenv("VESTRA_HIP_GEMM_TAIL", "0")
+    a = rt.download_f32(lin.run_chw(xt, rows))
+    e = rt.download_f32(rt.token_to_chw_f32(lin.run(xt, rows), rows, n))
+    assert_bits_equal(a, e, f"run_chw vs token_to_chw(run) {rows}x{k}->{n}")
+
+
 # M = 865 is one 504x336 image; 3460 = the batch of 4 (BASELINE config 5a) and
 # 3457 = one 1008x672 image (config 5b).  Past M = 1024 the GEMM takes other
 # tiles, an XCD-ordered tile walk and other split-K choices, so those paths

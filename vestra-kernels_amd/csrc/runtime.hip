@@ -1541,16 +1541,38 @@ extern "C" vh_status vh_linear_run_chw(const vh_linear *linear, const vh_tensor 
     const size_t len = rows * linear->L.N;
     if (rows == 0 || linear->L.N == 0)
         return mismatch(len, len, "vh_linear_run_chw: token_to_chw needs tokens and channels");
-    float *tmp = nullptr;
-    TRY(dalloc(s, len, &tmp, "GEMM output allocation"));
+    const Lin &L = linear->L;
     vh_tensor *t = nullptr;
     vh_status st = new_tensor(linear->rt, len, &t, "DPT CHW allocation");
-    if (!st) st = run_lin(s, linear->L, input->ptr, rows, vh::Epi::Store, tmp, "gemm_bias_scale");
-    if (!st)
-        st = launch(s, "token_to_chw", [&] {
-            return vh::launch_token_to_chw(s.stream, tmp, t->ptr, rows, linear->L.N);
-        });
-    hipFreeAsync(tmp, s.stream);
+    if (!st && !L.gamma && !L.ln_c && L.K % 32 == 0 && rows <= (size_t)INT32_MAX) {
+        // The transposed product in one GEMM: the weight rows [N][K] as A and
+        // the input rows as Bt, stored channel-major with the bias per
+        // channel by the implicit convolution's epilogue (a 1 x 1 tap over
+        // one image row of `rows` pixels); no token-major copy.
+        vh::GemmArgs g{};
+        g.a = L.wt;
+        g.bt = input->ptr;
+        g.m = L.N;
+        g.n = rows;
+        g.k = L.K;
+        g.epi = vh::Epi::Store;
+        g.c = t->ptr;
+        g.bias = L.bias;
+        g.conv_in_c = L.K;
+        g.conv_kw = 1;
+        g.conv_wp = rows;
+        g.conv_ow = rows;
+        st = launch(s, "gemm_bias_chw", [&] { return vh::launch_gemm(s.stream, g); });
+    } else if (!st) {
+        float *tmp = nullptr;
+        st = dalloc(s, len, &tmp, "GEMM output allocation");
+        if (!st) st = run_lin(s, L, input->ptr, rows, vh::Epi::Store, tmp, "gemm_bias_scale");
+        if (!st)
+            st = launch(s, "token_to_chw", [&] {
+                return vh::launch_token_to_chw(s.stream, tmp, t->ptr, rows, L.N);
+            });
+        if (tmp) hipFreeAsync(tmp, s.stream);
+    }
     if (st) {
         delete t;
         return st;
