@@ -186,6 +186,22 @@ def test_linear_run_chw_equals_token_to_chw_of_run(rt, monkeypatch, rows, k, n, 
     assert_bits_equal(a, e, f"run_chw vs token_to_chw(run) {rows}x{k}->{n}")
 
 
+@pytest.mark.parametrize("m,k,n", [(865, 768, 3072), (33, 96, 130), (1, 768, 3072), (70, 64, 257)])
+def test_gemm_row_major_b_in_place_equals_transposed_copy(rt, monkeypatch, m, k, n):
+    """gemm_row_major_f32 reads B [K][N] in place (the default at M, K <=
+    1024 with K % 32 == 0) or multiplies by a transposed copy
+    (VESTRA_HIP_GEMM_RM_DIRECT=0): with whole tiles on both routes they take
+    the same products in the same k order, so the same bits."""
+    a = rt.upload_f32(seeded.normal(7500 + m, m * k))
+    b = rt.upload_f32(seeded.normal(7600 + n, k * n, 0.05))
+    monkeypatch.setenv("VESTRA_HIP_GEMM_TAIL", "0")
+    outs = []
+    for route in ("1", "0"):
+        monkeypatch.setenv("VESTRA_HIP_GEMM_RM_DIRECT", route)
+        outs.append(rt.download_f32(rt.gemm_row_major_f32(a, b, m, k, n)))
+    assert_bits_equal(outs[0], outs[1], f"row-major GEMM {m}x{k}x{n}: B in place vs transposed")
+
+
 # M = 865 is one 504x336 image; 3460 = the batch of 4 (BASELINE config 5a) and
 # 3457 = one 1008x672 image (config 5b).  Past M = 1024 the GEMM takes other
 # tiles, an XCD-ordered tile walk and other split-K choices, so those paths

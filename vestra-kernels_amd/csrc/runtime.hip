@@ -985,6 +985,41 @@ extern "C" vh_status vh_gemm_row_major_f32(const vh_runtime *rt, const vh_tensor
     TRY(set_device(s));
     vh_tensor *t = nullptr;
     TRY(new_tensor(rt->s, mn, &t, "GEMM output allocation"));
+    // B read in place, K-major: the direct convolution's loader as a 1 x 1
+    // tap over a one-row "image" of n pixels and k channels, whose
+    // channel-major output is row-major C; no transposed copy of B.  Its
+    // eight 4-byte loads per thread and slice cost what the copy saves at
+    // M, K <= 1024 (per-launch events, 865 x 768 x 3072: 49.2 us against 39.3
+    // + 10.4 for the copy and the NT GEMM; per call, with the copy's
+    // allocation, 47.5 against 101.5 us), and lose beyond (865 x 3072 x 768
+    // 54.2 against 50.8, 3460 x 768 x 3072 167 against 140, 4096^3 1286
+    // against 1009).  VESTRA_HIP_GEMM_RM_DIRECT=0|1 forces either route.
+    const char *rm_env = std::getenv("VESTRA_HIP_GEMM_RM_DIRECT");
+    const bool rm_direct = rm_env ? rm_env[0] != '0' : (m <= 1024 && k <= 1024);
+    if (k > 0 && k % 32 == 0 && rm_direct) {
+        vh::GemmArgs g{};
+        g.a = a->ptr;
+        g.bt = b->ptr;
+        g.m = m;
+        g.n = n;
+        g.k = k;
+        g.epi = vh::Epi::Store;
+        g.c = t->ptr;
+        g.conv_in_c = k;
+        g.conv_kw = 1;
+        g.conv_ow = n;
+        g.conv_ih = 1;
+        g.conv_iw = n;
+        g.conv_stride = 1;
+        vh_status st = tail_workspace(s, g);
+        if (!st) st = launch(s, "gemm", [&] { return vh::launch_gemm(s.stream, g); });
+        if (st) {
+            delete t;
+            return st;
+        }
+        *out = t;
+        return VH_OK;
+    }
     float *bt = nullptr;
     vh_status st = dalloc(s, kn, &bt, "GEMM operand allocation");
     if (!st)
