@@ -735,17 +735,21 @@ def test_flash_key_layouts_deterministic_and_consistent(rt, monkeypatch):
             assert max_rel(a, outs[("1", "1", "1")]) <= 2e-6, (H, T, key)
 
 
+@pytest.mark.parametrize("xcd", ["1", "0"], ids=["xcd_grouped", "launch_order"])
 @pytest.mark.parametrize("token_major", [False, True], ids=["head_major", "token_major"])
-def test_flash_in_kernel_merge_equals_merge_launch(rt, monkeypatch, token_major):
+def test_flash_in_kernel_merge_equals_merge_launch(rt, monkeypatch, token_major, xcd):
     """Key splits merged by the split that finishes last in each 64-query
     group (VESTRA_HIP_FLASH_FUSED=1; the default when the grid is one round
     of workgroups) equal, bit for bit, the same splits merged by the separate
     merge launch (=0), at 2, 3 and 4 splits, for full and partial last query
     tiles and for grids of one round (12 x 865 at 2 and 3 splits) and of
-    several (48 x 865).  Each shape runs three times,
+    several (48 x 865).  In launch order (VESTRA_HIP_FLASH_XCD=0) the splits
+    of a query group sit on different XCDs, whose L2s do not see each
+    other's writes: the publication must go through the agent-scope path.  Each shape runs three times,
     every output kept alive so that no run lands in an earlier run's memory:
     the arrival counters must be back at zero after every run, or a later
     run would merge early or leave rows unwritten."""
+    monkeypatch.setenv("VESTRA_HIP_FLASH_XCD", xcd)
     for H, T in ((12, 865), (48, 865), (1, 130), (3, 200), (2, 257)):
         n = H * T * 64
         q, k, v = (rt.upload_f32(seeded.normal(s + 7 * T + H, n)) for s in (41, 42, 43))
