@@ -21,7 +21,12 @@ exercised with its neighbours.  Bars:
   head dims 16 to 128 and the resizes bit for bit, the two-pass LayerNorm
   within 1e-5, convolutions (any kernel size, stride and padding) and
   transposed convolutions within twice the f32 accumulation bound of the
-  direct definition, bit for bit where the gather form applies.
+  direct definition, bit for bit where the gather form applies;
+- the routes that read a CHW or K-major operand in place (channel counts
+  that are multiples of 32): direct convolutions, including small grids
+  whose K is split past four pieces, transposed convolutions with
+  kernel == stride, and gemm_row_major_f32 at M, K <= 1024, against the
+  same bounds.
 """
 import numpy as np
 import pytest
@@ -59,6 +64,8 @@ Q8_CASES = [(_dim(1, 2000), _dim(1, 2100), 32 * int(_RNG.integers(1, 80)),
 ELEMENTWISE_CASES = [(str(op), int(_RNG.integers(1, 1 << 30)))
                      for op in _RNG.permutation(["gelu", "layernorm", "quantize", "rope", "resize",
                                                  "conv", "conv_transpose"] * 3)]
+IN_PLACE_CASES = [(str(op), int(_RNG.integers(1, 1 << 30)))
+                  for op in _RNG.permutation(["conv", "conv_transpose", "row_major"] * 4)]
 
 
 @pytest.mark.parametrize("mode, m, k, n, gamma, seed", PROJ_CASES)
@@ -214,3 +221,47 @@ def test_elementwise_random_shapes_vs_oracle(rt, op, seed):
             assert np.all(np.abs(got.astype(np.float64) - exp) <= 2 * (in_c + 2) * 6e-8 * absb + 1e-30)
         else:
             assert_bits_equal(got, exp, f"gather transposed conv k{kk} s{s}")
+
+
+@pytest.mark.parametrize("op, seed", IN_PLACE_CASES)
+def test_in_place_operand_routes_random_shapes(rt, op, seed):
+    rng = np.random.default_rng(seed)
+    if op == "conv":
+        in_c, out_c = 32 * int(rng.integers(1, 25)), int(rng.integers(1, 200))
+        kk, s = int(rng.choice([1, 3, 3, 5])), int(rng.choice([1, 1, 2]))
+        p = int(rng.integers(0, kk // 2 + 2))
+        ih, iw = int(rng.integers(kk, 40)), int(rng.integers(kk, 40))
+        x = rng.standard_normal(in_c * ih * iw).astype(np.float32)
+        w = (rng.standard_normal(out_c * in_c * kk * kk) / np.sqrt(in_c * kk * kk)).astype(np.float32)
+        b = rng.standard_normal(out_c).astype(np.float32)
+        got = rt.download_f32(rt.prepare_conv2d_f32(in_c, out_c, kk, kk, s, p, w, b).run(
+            rt.upload_f32(x), ih, iw))
+        exp = O.conv2d_naive(x, in_c, ih, iw, w, out_c, kk, kk, s, p, b)
+        absb = O.conv2d_naive(np.abs(x), in_c, ih, iw, np.abs(w), out_c, kk, kk, s, p, np.abs(b))
+        assert np.all(np.abs(got.astype(np.float64) - exp) <=
+                      2 * (in_c * kk * kk + 2) * 6e-8 * absb.astype(np.float64) + 1e-30)
+    elif op == "conv_transpose":
+        in_c, out_c = 32 * int(rng.integers(1, 13)), int(rng.integers(1, 100))
+        kk = int(rng.choice([2, 3, 4]))
+        ih, iw = int(rng.integers(1, 30)), int(rng.integers(1, 30))
+        x = rng.standard_normal(in_c * ih * iw).astype(np.float32)
+        w = (rng.standard_normal(in_c * out_c * kk * kk) / np.sqrt(in_c)).astype(np.float32)
+        b = rng.standard_normal(out_c).astype(np.float32)
+        got = rt.download_f32(rt.conv_transpose2d_f32(rt.upload_f32(x), in_c, ih, iw, w, out_c, kk,
+                                                      kk, kk, b))
+        exp = O.conv_transpose2d_naive(x, in_c, ih, iw, w, out_c, kk, kk, kk, b)
+        absb = O.conv_transpose2d_naive(np.abs(x), in_c, ih, iw, np.abs(w), out_c, kk, kk, kk,
+                                        np.abs(b))
+        assert np.all(np.abs(got.astype(np.float64) - exp) <= 2 * (in_c + 2) * 6e-8 * absb + 1e-30)
+    else:
+        m, k, n = _rand_dim(rng, 1, 1024), 32 * int(rng.integers(1, 33)), _rand_dim(rng, 1, 3000)
+        a = rng.standard_normal(m * k).astype(np.float32)
+        bm = (rng.standard_normal(k * n) * 0.05).astype(np.float32)
+        got = rt.download_f32(rt.gemm_row_major_f32(rt.upload_f32(a), rt.upload_f32(bm), m, k, n))
+        ref = a.reshape(m, k).astype(np.float64) @ bm.reshape(k, n).astype(np.float64)
+        bound = (k + 2) * 6e-8 * (np.abs(a.reshape(m, k)).astype(np.float64) @ np.abs(bm.reshape(k, n)))
+        assert np.all(np.abs(got.reshape(m, n) - ref) <= bound + 1e-30)
+
+
+def _rand_dim(rng, lo, hi):
+    return int(rng.integers(lo, hi + 1)) if rng.random() < 0.5 else int(min(hi, 32 * rng.integers(1, hi // 32 + 1)))
